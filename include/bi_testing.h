@@ -1,0 +1,46 @@
+/*
+ * bi_testing.h -- introspection entry points of libbi.so used by the test
+ * suite and the benchmark. They have no counterpart in the reference, whose
+ * GEMM has a single output tile (reference _gemm.py:25-27).
+ *
+ * libbi.so builds its GEMM as a small table of workgroup output footprints
+ * ("geometries": rows x columns of C per workgroup, waves per workgroup). All
+ * of them execute the same per-element arithmetic: the same MFMA instruction
+ * on the same K-chunks in the same ascending order, then the same epilogue.
+ * bi_gemm picks a geometry from (M, N) alone to fill the GPU. These entry
+ * points let a test run one input through every geometry and compare bits,
+ * which is the direct proof that the footprint choice cannot change a result.
+ */
+#ifndef BI_TESTING_H
+#define BI_TESTING_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Number of GEMM geometries built into the library. */
+int bi_gemm_num_geometries(void);
+
+/* Describes geometry `g`: rows and columns of C per workgroup and waves per
+ * workgroup. Returns BI_EINVAL for an unknown g. */
+int bi_gemm_geometry_info(int g, int* block_m, int* block_n, int* waves);
+
+/* The geometry bi_gemm would launch for this problem. */
+int bi_gemm_pick_geometry(int64_t M, int64_t N, int64_t K, int dtype, int trans_b);
+
+/* bi_gemm with the geometry forced to `g` (same arguments and semantics). */
+int bi_gemm_with_geometry(const void* a, const void* b, const void* bias, void* out,
+                          int64_t M, int64_t N, int64_t K, int dtype, int trans_b,
+                          float alpha, float beta, int g, void* hip_stream);
+
+/* Wavefront width the kernels were compiled for (64 on gfx950); the fixed
+ * reduction shapes assume it. Reads a device-side constant: needs a GPU. */
+int bi_device_wavefront_size(int* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BI_TESTING_H */
