@@ -1,0 +1,257 @@
+"""Benchmark of the batch-invariant GEMM + SDPA hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (the GEMM sweep, at M = 256 where the
+roofline target applies): one step = bi.matmul over the five (K, N) shapes of
+the sweep, (256, K) bf16 activations ~ N(0, 1) times (K, N) bf16 weights
+~ N(0, 1/K), seeded. `value` is the step's total flops / wall time, inputs
+resident in HBM. Alongside, on the same run:
+  * roofline of the dominant kernel (256 x 4096 x 32000), its average
+    duration measured with HIP events on the launch stream;
+  * stock torch.matmul (hipBLASLt) on the same inputs, interleaved;
+  * decode SDPA (configs[2]: B = 64, 32/8 heads, D = 128, N = 8192) GB/s;
+  * a bit-invariance check of one row across batch sizes 1..256;
+  * the CPU baseline: the oracle's fixed-order fp32 restatement of the
+    reference GEMM (C, OpenMP) on a bounded sample of the same workload.
+Prints one JSON line.
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "mlx-batch-invariant_amd"), REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "bi-GEMM TFLOP/s & SDPA GB/s vs roofline; 0 bits differ across batch 1-256"
+M = 256
+SHAPES = [(512, 512), (4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)]  # (K, N)
+DOMINANT = (4096, 32000)
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+SDPA = dict(B=64, H=32, Hkv=8, N=8192, D=128)
+CPU_ROWS = 256              # rows of M per shape in the CPU sample (all of them)
+CPU_SECONDS = 10.0          # repeat whole passes until at least this long
+
+
+def gemm_flops(m, k, n):
+    return 2.0 * m * k * n
+
+
+def gemm_bytes(m, k, n, esize=2):
+    return float(m * k + k * n + m * n) * esize
+
+
+def sdpa_bytes(B, H, Hkv, N, D, esize=2):
+    return float(2 * B * Hkv * N * D + 2 * B * H * 1 * D) * esize
+
+
+def make_inputs(torch, dev):
+    g = torch.Generator().manual_seed(0)
+    ops = []
+    for K, N in SHAPES:
+        a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+        w = (torch.randn(K, N, generator=g) / math.sqrt(K)).to(torch.bfloat16)
+        ops.append((a, w, a.to(dev), w.to(dev)))
+    return ops
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel, measured with rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE and scaled by a copy-kernel calibration; the
+    summary is committed under profiles/. None when absent."""
+    path = os.path.join(REPO, "profiles", "gemm_bf16_256x4096x32000_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(ops):
+    """Oracle fixed-order fp32 GEMM (C, OpenMP, all usable cores up to 16) on
+    the first CPU_ROWS rows of every shape of the step."""
+    cores = min(16, len(os.sched_getaffinity(0)))
+    os.environ["OMP_NUM_THREADS"] = str(cores)
+    import numpy as np
+
+    from oracle import gemm as ogemm
+
+    lib = ogemm.clib()
+    prepared = []
+    for a, w, _, _ in ops:
+        a32 = np.ascontiguousarray(a[:CPU_ROWS].float().numpy())
+        bt = np.ascontiguousarray(w.float().numpy().T)  # (N, K): contiguous inner loop
+        prepared.append((a32, bt, np.empty((CPU_ROWS, bt.shape[0]), dtype=np.float32)))
+    flops, passes = 0.0, 0
+    t0 = time.perf_counter()
+    while passes == 0 or time.perf_counter() - t0 < CPU_SECONDS:
+        for a32, bt, out in prepared:
+            lib.oracle_gemm_bt(ogemm.fptr(a32), ogemm.fptr(bt), ogemm.fptr(out), CPU_ROWS,
+                               bt.shape[0], a32.shape[1])
+            flops += gemm_flops(CPU_ROWS, a32.shape[1], bt.shape[0])
+        passes += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": cores,
+            "kind": "port",
+            "sample": "%d pass(es) over the first %d of the %d rows of each of the 5 (K,N) "
+                      "shapes; fixed-order fp32 fmaf restatement of the reference K loop "
+                      "(oracle/csrc/oracle.c), %.1f s" % (passes, CPU_ROWS, M, dt)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device-to-device copy three times (the known-size "
+                         "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the invariant GEMM and attention have no "
+              "multi-GPU path in this build (--gpus %d requested)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import mlx_batch_invariant as bi
+    from mlx_batch_invariant import _gemm
+    from oracle.bits import bits
+
+    dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes": src.numel() * 4}))
+        return
+    ops = make_inputs(torch, dev)
+    step_flops = sum(gemm_flops(M, K, N) for K, N in SHAPES)
+    dom = SHAPES.index(DOMINANT)
+
+    def step(outs=None):
+        for i, (_, _, a, w) in enumerate(ops):
+            y = bi.matmul(a, w)
+            if outs is not None:
+                outs.append(y)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly --steps steps, synchronised on both sides; the
+    # dominant kernel is bracketed by events on the launch stream.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        for i, (_, _, a, w) in enumerate(ops):
+            if i == dom:
+                evs[s][0].record()
+                bi.matmul(a, w)
+                evs[s][1].record()
+            else:
+                bi.matmul(a, w)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = step_flops * args.steps / elapsed / 1e12
+    dom_us = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3
+
+    # Per-shape and stock comparison (HIP events, interleaved A/B, median of 9).
+    def time_us(fn, reps=20):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    per_shape = []
+    for (K, N), (_, _, a, w) in zip(SHAPES, ops):
+        bi_t, st_t = [], []
+        for _ in range(9):
+            bi_t.append(time_us(lambda: bi.matmul(a, w)))
+            st_t.append(time_us(lambda: torch.matmul(a, w)))
+        tb, ts = statistics.median(bi_t), statistics.median(st_t)
+        per_shape.append({"M": M, "K": K, "N": N, "bi_us": round(tb, 2),
+                          "bi_tflops": round(gemm_flops(M, K, N) / tb / 1e6, 1),
+                          "stock_us": round(ts, 2),
+                          "stock_tflops": round(gemm_flops(M, K, N) / ts / 1e6, 1),
+                          "geometry": _gemm.geometries()[
+                              _gemm._lib.lib().bi_gemm_pick_geometry(M, N, K, 2, 0)]})
+
+    # Roofline of the dominant kernel: AI below the bf16 ridge, so HBM binds.
+    Kd, Nd = DOMINANT
+    fl, by = gemm_flops(M, Kd, Nd), gemm_bytes(M, Kd, Nd)
+    hbm_achieved = by / dom_us / 1e3  # GB/s
+    roof = {"bound": "hbm", "achieved": round(hbm_achieved, 1), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(hbm_achieved / PEAK_HBM_GBS, 4),
+            "traffic": load_traffic(),
+            "kernel": "bi_gemm bf16 %dx%dx%d (K,N) layout" % (M, Kd, Nd),
+            "avg_launch_us": round(dom_us, 2),
+            "mfma_achieved_tflops": round(fl / dom_us / 1e6, 1),
+            "mfma_frac": round(fl / dom_us / 1e6 / PEAK_BF16_TFLOPS, 4),
+            "frac_of_min_roof": round((fl / dom_us / 1e6) /
+                                      min(PEAK_BF16_TFLOPS, fl / by * PEAK_HBM_GBS / 1e3), 4)}
+
+    # Decode SDPA.
+    g = torch.Generator().manual_seed(0)
+    B, H, Hkv, N, D = SDPA["B"], SDPA["H"], SDPA["Hkv"], SDPA["N"], SDPA["D"]
+    q = torch.randn(B, H, 1, D, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(B, Hkv, N, D, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(B, Hkv, N, D, generator=g).to(torch.bfloat16).to(dev)
+    sc = 1.0 / math.sqrt(D)
+    sd_bi = statistics.median(time_us(lambda: bi.scaled_dot_product_attention(q, k, v, scale=sc),
+                                      reps=10) for _ in range(5))
+    sd_st = statistics.median(time_us(lambda: torch.nn.functional.scaled_dot_product_attention(
+        q, k, v, scale=sc, enable_gqa=True), reps=10) for _ in range(5))
+    sbytes = sdpa_bytes(B, H, Hkv, N, D)
+    sdpa = {"config": dict(SDPA, qL=1, dtype="bf16"), "bi_us": round(sd_bi, 1),
+            "gbps": round(sbytes / sd_bi / 1e3, 1), "stock_us": round(sd_st, 1),
+            "stock_gbps": round(sbytes / sd_st / 1e3, 1),
+            "roofline": {"bound": "hbm", "achieved": round(sbytes / sd_bi / 1e3, 1),
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(sbytes / sd_bi / 1e3 / PEAK_HBM_GBS, 4)}}
+
+    # Invariance spot check: row 0 of the (4096, 4096) shape across batch sizes.
+    a, w = ops[1][2], ops[1][3]
+    ref = bits(bi.matmul(a[:1].contiguous(), w)[0])
+    differing = 0
+    for b in (2, 3, 8, 16, 33, 64, 128, 256):
+        differing += int((bits(bi.matmul(a[:b].contiguous(), w)[0]) != ref).sum())
+
+    cpu = None if args.no_cpu else cpu_baseline(ops)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[1] GEMM sweep at M=256, bf16, bi.matmul (K,N) weights",
+                   "M": M, "shapes_KN": SHAPES, "parallelism": "none (one GPU)"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "per_shape": per_shape,
+        "sdpa_decode": sdpa,
+        "invariance_bits_differing_batch_1_to_256": differing,
+        "device": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,7 @@
+// GEMM kernels for float operands (one translation unit per element type so the
+// instantiations compile in parallel).
+#include "bi_gemm_kernel.h"
+
+bi_gemm_dev::KernelFn bi_gemm_kernel_f32(int g, bool trans_b) {
+  return bi_gemm_dev::kernel_for<float>(g, trans_b);
+}

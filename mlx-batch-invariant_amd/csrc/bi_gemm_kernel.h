@@ -1,0 +1,586 @@
+// Device code of the batch-invariant GEMM (gfx950); included by the
+// per-element-type translation units bi_gemm_{f32,f16,bf16}.hip.
+//
+// Restates the reference bi_gemm (mlx_batch_invariant/_gemm.py:29-130): one
+// workgroup owns an output tile and the whole K reduction for it, the K-loop
+// trip count depends on K alone, tiles are staged through LDS, and the bias is
+// added to the fp32 accumulator before the single rounding to the element type
+// (_gemm.py:115-129). No split-K, no atomics.
+//
+// Fixed per-element arithmetic (the invariance contract):
+//   * K is consumed in chunk-steps q = 0, 1, 2, ... in ascending order, exactly
+//     ceil(K / 32) of them for bf16/f16 and ceil(K / 16) for fp32 -- a function
+//     of K alone. Elements past K read as zero.
+//       bf16/f16: chunk-step q is one v_mfma_f32_16x16x32_{bf16,f16}; lane
+//                 group g = lane / 16 supplies k = 32q + 8g + t, t = 0..7.
+//       fp32:     chunk-step q is four v_mfma_f32_16x16x4_f32, t = 0..3; lane
+//                 group g supplies k = 16q + 4g + t. Chunk-step q accumulates
+//                 into chain q mod 2 (two chains halve the length of each fp32
+//                 accumulation) and acc = chain_0 + chain_1.
+//     Every output element sees exactly this sequence of MFMAs on its own row
+//     of A and column of B, each chain starting from +0.0.
+//   * Epilogue: v = bias ? fma(alpha, acc, beta * bias[n]) : acc, then one
+//     round-to-nearest-even to the element type.
+// The workgroup footprint (rows x columns of C per workgroup, waves, pipeline
+// depth, bytes staged per step) comes from a table of compile-time geometries
+// that all run this same sequence per element; it only decides how many
+// elements a workgroup owns and how their operands travel. An output row
+// therefore has the same bits whatever M is, whatever rows surround it,
+// whichever slot of a tile it lands in, and whichever geometry the launch
+// picked.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bi_internal.h"
+
+namespace bi_gemm_dev {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+struct GemmArgs {
+  const void* a;
+  const void* b;
+  const void* bias;
+  void* out;
+  int64_t M, N, K;
+  int tiles_m, tiles_n;
+  float alpha, beta;
+  int vec_a, vec_b;  // rows of A / rows of B may be read as aligned 16-byte vectors
+};
+
+// ---------------------------------------------------------------- element types
+
+template <typename T> struct Elem;
+template <> struct Elem<__bf16> {
+  __device__ static float to_f32(__bf16 x) { return (float)x; }
+  __device__ static __bf16 from_f32(float x) { return (__bf16)x; }  // RNE
+};
+template <> struct Elem<_Float16> {
+  __device__ static float to_f32(_Float16 x) { return (float)x; }
+  __device__ static _Float16 from_f32(float x) { return (_Float16)x; }  // RNE
+};
+template <> struct Elem<float> {
+  __device__ static float to_f32(float x) { return x; }
+  __device__ static float from_f32(float x) { return x; }
+};
+
+// One chunk-step of the fixed arithmetic for a 16x16 output block: `a` and
+// `b` are this lane's 16-byte operand chunks.
+__device__ inline f32x4_t chunk_step(__bf16, uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+__device__ inline f32x4_t chunk_step(_Float16, uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+__device__ inline f32x4_t chunk_step(float, uint4 a, uint4 b, f32x4_t c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), c, 0, 0, 0);
+  return c;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
+// Remap so that consecutive logical tiles -- which share operand panels -- run
+// on the same XCD.
+__device__ inline int xcd_remap(int w, int total) {
+  const int per = total >> 3;
+  if (w < (per << 3)) return (w & 7) * per + (w >> 3);
+  return w;
+}
+
+// 16-byte chunk of row `row` of a row-major matrix with leading dimension
+// `ld`, starting at element k, read element by element; elements of rows at
+// or past `rows` or at or past column `limit` are zero. The path for operands
+// the buffer path cannot take (unaligned, or panels of 2 GiB and more).
+template <typename T>
+__device__ inline uint4 load_chunk(const T* __restrict__ base, int64_t row, int64_t rows,
+                                   int64_t ld, int64_t k, int64_t limit) {
+  constexpr int E = 16 / sizeof(T);
+  const bool row_ok = row < rows;
+  union {
+    uint4 u;
+    T e[E];
+  } r;
+  const T* p = base + (row_ok ? row : 0) * ld;
+#pragma unroll
+  for (int i = 0; i < E; i++) r.e[i] = (row_ok && k + i < limit) ? p[k + i] : T(0);
+  return r.u;
+}
+
+// Raw buffer resources (CDNA "V#"): loads whose byte offset is at or past
+// num_records return zero in hardware, so out-of-range rows and K/N tails cost
+// no branch. dword3 0x00020000 selects the untyped 32-bit format used by raw
+// buffer accesses on the gfx9 family.
+constexpr uint32_t kOutOfRange = 0x80000000u;  // >= every num_records used below
+// The base and size are workgroup-uniform; readfirstlane states that to the
+// compiler, which otherwise may wrap every buffer access in a loop over the
+// distinct descriptors of the wave.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int32_t n = bytes < (int64_t)kOutOfRange ? (int32_t)bytes : (int32_t)(kOutOfRange - 1);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, __builtin_amdgcn_readfirstlane(n),
+                                           0x00020000);
+}
+__device__ inline uint4 buffer_chunk(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// Chunk swizzles: 16-byte chunk c of LDS row r is stored at chunk position
+// c ^ swz(r) so that the MFMA operand reads of 16 consecutive rows spread over
+// the LDS banks.
+__device__ inline int swz_k(int r) { return r & 7; }  // [rows][>= 8 chunks] tiles
+template <typename T, int CPR>
+__device__ inline int swz_nn(int k) {  // [k][CPR chunks] tiles (B in (K, N) layout)
+  if constexpr (sizeof(T) == 2)
+    return (((k & 3) << 1) | (((k >> 3) & 1) << 3)) & (CPR - 1);
+  else
+    return (((k >> 2) & 3) << 2) & (CPR - 1);
+}
+
+// s_waitcnt immediate (gfx9 encoding): wait until at most `vm` vector-memory
+// operations of this wave are outstanding and all LDS operations completed.
+constexpr int waitcnt_vm_lgkm0(int vm) {
+  return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (0x0 << 8);
+}
+
+// One workgroup computes a BM x BN tile of C over the whole of K.
+//   WM x WN compute waves own (BM / WM) x (BN / WN) sub-tiles; NW >= WM * WN
+//   waves in total, the extra waves only load.
+//   KB: bytes of each A / B row staged per pipeline stage (a multiple of 128).
+//   NS: stages in the LDS ring. Operands move global -> LDS with buffer loads
+//       that write LDS directly (no VGPR staging, no ds_write); NS - 1 stages
+//       are in flight while one is computed. One barrier per stage.
+// The pipeline shape never changes what an output element computes: every
+// geometry issues the same chunk-steps in the same order (see file header).
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB>
+struct GemmTile {
+  static constexpr int NT = 64 * NW;
+  static constexpr int CW = WM * WN;                  // compute waves
+  static constexpr int EPC = 16 / sizeof(T);          // elements per 16-byte chunk
+  static constexpr int RC = KB / 16;                  // chunks per tile row per stage
+  static constexpr int EPS = KB / sizeof(T);          // elements of K per stage
+  static constexpr int CS = KB / 64;                  // chunk-steps per stage
+  static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  static constexpr int FM = WTM / 16, FN = WTN / 16;  // 16x16 MFMA blocks per wave
+  static constexpr int A_CH = BM * RC;                // chunks per stage
+  static constexpr int B_CH = BN * RC;
+  static constexpr int LA = (A_CH + NT - 1) / NT;     // chunks per thread per stage (VGPR path)
+  static constexpr int LB = (B_CH + NT - 1) / NT;
+  static constexpr int NN_CPR = BN * (int)sizeof(T) / 16;  // chunks per k-row, (K, N) B tile
+  static constexpr int STAGE_CH = A_CH + B_CH;
+  static constexpr int DMA = STAGE_CH / 64 / NW;      // 1 KB LDS-DMA loads per wave per stage
+  static constexpr int CHAINS = sizeof(T) == 4 ? 2 : 1;    // fp32: chain per chunk-step parity
+  static_assert(CW <= NW && FM >= 1 && FN >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "geometry");
+  static_assert(KB % 128 == 0 && CS % 2 == 0, "stage bytes");
+  static_assert(TB || (NN_CPR >= 1 && (NN_CPR & (NN_CPR - 1)) == 0), "bad (K,N) tile width");
+  static constexpr int DMA_A = A_CH / 64 / NW;      // of which A loads (the rest load B)
+  static_assert(A_CH % (64 * NW) == 0 && B_CH % (64 * NW) == 0, "stage must split into 1 KB loads");
+  static_assert(NS >= 2 && NS <= 8 && DMA * (NS - 2) <= 63, "ring depth");
+
+  const T* __restrict__ A;
+  const T* __restrict__ B;
+  int64_t M, N, K, m0, n0;
+  int tid, wave, lane, g, r16, wm, wn;
+  // Buffer path: the A panel (rows m0.. of A), the B panel (rows n0.. of an
+  // (N, K) B, or columns n0.. of a (K, N) B); bytes past the valid rows are
+  // outside num_records.
+  __amdgpu_buffer_rsrc_t ra_src, rb_src;
+
+  __device__ __forceinline__ void init_buffers() {
+    constexpr int64_t E = sizeof(T);
+    ra_src = make_rsrc(A + m0 * K, min((int64_t)BM, M - m0) * K * E);
+    if constexpr (TB)
+      rb_src = make_rsrc(B + n0 * K, min((int64_t)BN, N - n0) * K * E);
+    else
+      rb_src = make_rsrc(B + n0, (K * N - n0) * E);
+  }
+
+  // Per-lane DMA addressing, fixed for the whole K loop. Load i of this wave
+  // fills the 64 LDS chunks starting at chunk blk(i) * 64, one per lane; LDS
+  // rows are swizzled, so the lane's position holds logical chunk
+  // phys ^ swz(row). For stage s the lane loads panel byte offset
+  // base[i] + s * step (step = EPS elements along K, or EPS rows of a (K, N)
+  // B), provided its K index kidx[i] + s * EPS is below K (and, for a (K, N)
+  // B, its column is inside N); otherwise it loads zeros.
+  uint32_t dma_base[DMA];
+  int32_t dma_kidx[DMA];
+
+  __device__ __forceinline__ int dma_blk(int i) const {
+    return i < DMA_A ? i * NW + wave : (i - DMA_A) * NW + wave;
+  }
+
+  __device__ __forceinline__ void init_dma() {
+    constexpr uint32_t E = sizeof(T);
+#pragma unroll
+    for (int i = 0; i < DMA; i++) {
+      const int p = dma_blk(i) * 64 + lane;  // chunk position within the A or B region
+      if (i < DMA_A || TB) {
+        const int r = p / RC, c = (p % RC) ^ swz_k(r);
+        dma_base[i] = (uint32_t)(r * K + c * EPC) * E;
+        dma_kidx[i] = c * EPC;
+      } else {
+        const int kr = p / NN_CPR, c = (p % NN_CPR) ^ swz_nn<T, NN_CPR>(kr);
+        const int n = c * EPC;
+        dma_base[i] = (uint32_t)(kr * N + n) * E;
+        // A column outside N never loads: push its K index out of range.
+        dma_kidx[i] = (n0 + n < N) ? kr : INT32_MAX / 2;
+      }
+    }
+  }
+
+  // Issue this wave's LDS-DMA loads of stage s into `slot`.
+  __device__ __forceinline__ void dma(int64_t s, uint4* __restrict__ slot) const {
+    constexpr uint32_t E = sizeof(T);
+    const int32_t kleft = (int32_t)(K - s * EPS);  // K elements from this stage on
+    const uint32_t a_step = (uint32_t)(s * EPS) * E;
+    const uint32_t b_step = TB ? a_step : (uint32_t)(s * EPS * N) * E;
+#pragma unroll
+    for (int i = 0; i < DMA; i++) {
+      const bool is_a = i < DMA_A;
+      lds_void_t* dst = (lds_void_t*)(slot + (is_a ? 0 : A_CH) + dma_blk(i) * 64);
+      const uint32_t off = dma_kidx[i] < kleft ? dma_base[i] + (is_a ? a_step : b_step) : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? ra_src : rb_src, dst, 16, off, 0, 0, 0);
+    }
+  }
+
+  // Register-staged loads for operands the buffer path cannot take.
+  __device__ __forceinline__ void gload_slow(int64_t s, uint4* ra, uint4* rb) const {
+    const int64_t k0 = s * EPS;
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+      const int q = tid + i * NT;
+      if (A_CH % NT == 0 || q < A_CH)
+        ra[i] = load_chunk<T>(A, m0 + q / RC, M, K, k0 + (q % RC) * EPC, K);
+    }
+#pragma unroll
+    for (int i = 0; i < LB; i++) {
+      const int q = tid + i * NT;
+      if (B_CH % NT == 0 || q < B_CH) {
+        if constexpr (TB)
+          rb[i] = load_chunk<T>(B, n0 + q / RC, N, K, k0 + (q % RC) * EPC, K);
+        else
+          rb[i] = load_chunk<T>(B, k0 + q / NN_CPR, K, N, n0 + (q % NN_CPR) * EPC, N);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void sstore(uint4* As, const uint4* ra, const uint4* rb) const {
+    uint4* Bs = As + A_CH;
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+      const int q = tid + i * NT;
+      if (A_CH % NT == 0 || q < A_CH) {
+        const int r = q / RC, c = q % RC;
+        As[r * RC + (c ^ swz_k(r))] = ra[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < LB; i++) {
+      const int q = tid + i * NT;
+      if (B_CH % NT == 0 || q < B_CH) {
+        if constexpr (TB) {
+          const int r = q / RC, c = q % RC;
+          Bs[r * RC + (c ^ swz_k(r))] = rb[i];
+        } else {
+          const int r = q / NN_CPR, c = q % NN_CPR;
+          Bs[r * NN_CPR + (c ^ swz_nn<T, NN_CPR>(r))] = rb[i];
+        }
+      }
+    }
+  }
+
+  // B operand chunk for chunk-step j of the 16-column block at tile column nb.
+  __device__ __forceinline__ uint4 load_b(const uint4* __restrict__ Bs, int j, int nb) const {
+    if constexpr (TB) {
+      const int r = nb + r16;
+      return Bs[r * RC + ((4 * j + g) ^ swz_k(r))];
+    } else if constexpr (sizeof(T) == 2) {
+      // ds_read_tr16_b64: in each 16-lane group, lane i receives element
+      // (row 4t + i/4, column i%4) of the 16 x (4 x 16-bit) rows addressed by
+      // the group's lanes. Lane r16 addresses k-row kb + r16/4 at column
+      // nb + 4 * (r16 % 4), so lane i receives B[kb + t][nb + i], t = 0..3.
+      uint2 h[2];
+#pragma unroll
+      for (int half = 0; half < 2; half++) {
+        const int kr = 32 * j + 8 * g + 4 * half + (r16 >> 2);
+        const int col = nb + 4 * (r16 & 3);
+        const int chunk = (col >> 3) ^ swz_nn<T, NN_CPR>(kr);
+        const char* addr =
+            reinterpret_cast<const char*>(Bs) + (kr * NN_CPR + chunk) * 16 + (col & 7) * 2;
+        i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(addr));
+        h[half] = __builtin_bit_cast(uint2, v);
+      }
+      return make_uint4(h[0].x, h[0].y, h[1].x, h[1].y);
+    } else {
+      // fp32: element t of the chunk is B[16j + 4g + t][nb + r16].
+      const float* Bf = reinterpret_cast<const float*>(Bs);
+      uint32_t e[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int kr = 16 * j + 4 * g + t;
+        const int col = nb + r16;
+        const int chunk = (col >> 2) ^ swz_nn<T, NN_CPR>(kr);
+        e[t] = __float_as_uint(Bf[(kr * NN_CPR + chunk) * 4 + (col & 3)]);
+      }
+      return make_uint4(e[0], e[1], e[2], e[3]);
+    }
+  }
+
+  __device__ __forceinline__ void read_operands(const uint4* __restrict__ As, int j, uint4 (&av)[FM],
+                                                uint4 (&bv)[FN]) const {
+    const uint4* Bs = As + A_CH;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      const int r = wm * WTM + i * 16 + r16;
+      av[i] = As[r * RC + ((4 * j + g) ^ swz_k(r))];
+    }
+#pragma unroll
+    for (int jn = 0; jn < FN; jn++) bv[jn] = load_b(Bs, j, wn * WTN + jn * 16);
+  }
+
+  // All CS chunk-steps of the stage held in LDS at `As`, for every block of
+  // this wave; operands of step j + 1 are read while step j's MFMAs run.
+  __device__ __forceinline__ void compute_full(const uint4* __restrict__ As,
+                                               f32x4_t (&acc)[CHAINS][FM][FN]) const {
+    uint4 av[2][FM], bv[2][FN];
+    read_operands(As, 0, av[0], bv[0]);
+#pragma unroll
+    for (int j = 0; j < CS; j++) {
+      if (j + 1 < CS) read_operands(As, j + 1, av[(j + 1) & 1], bv[(j + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int jn = 0; jn < FN; jn++)
+          acc[j % CHAINS][i][jn] =
+              chunk_step(T(0), av[j & 1][i], bv[j & 1][jn], acc[j % CHAINS][i][jn]);
+    }
+  }
+
+  // The first `steps` (< CS) chunk-steps of the last stage.
+  __device__ __forceinline__ void compute_part(const uint4* __restrict__ As, int steps,
+                                               f32x4_t (&acc)[CHAINS][FM][FN]) const {
+#pragma unroll
+    for (int j = 0; j < CS - 1; j++) {
+      if (j < steps) {
+        uint4 av[FM], bv[FN];
+        read_operands(As, j, av, bv);
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int jn = 0; jn < FN; jn++)
+            acc[j % CHAINS][i][jn] = chunk_step(T(0), av[i], bv[jn], acc[j % CHAINS][i][jn]);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void compute(const uint4* __restrict__ As, int steps,
+                                          f32x4_t (&acc)[CHAINS][FM][FN]) const {
+    if (steps == CS)
+      compute_full(As, acc);
+    else if (steps > 0)
+      compute_part(As, steps, acc);
+  }
+
+  __device__ __forceinline__ int steps_of(int64_t nsteps, int64_t s) const {
+    const int64_t left = nsteps - s * CS;
+    return left <= 0 ? 0 : (left < CS ? (int)left : CS);
+  }
+
+  // Buffer path. The ring slots are distinct LDS arrays indexed at compile
+  // time, which lets the compiler see that reading slot u does not depend on
+  // the DMA still landing in the other slots; the waits are explicit: before
+  // computing stage s, this wave's loads of stages s+1 .. s+NS-2 may still be
+  // in flight, then a barrier makes every wave's part of stage s visible and
+  // guarantees the slot about to be refilled is no longer read.
+  // The steady state has no branches: whole rounds of NS stages whose chunk-
+  // steps are all inside K. A tail round handles the partial last stage;
+  // stages past K load zeros and compute nothing.
+  template <bool COMPUTE, typename Slots>
+  __device__ __forceinline__ void dma_rounds(const Slots& slots, int64_t nst, int64_t nsteps,
+                                             f32x4_t (&acc)[CHAINS][FM][FN]) const {
+    const int64_t full_rounds = (nsteps / CS) / NS;
+    int64_t s0 = 0;
+    for (int64_t r = 0; r < full_rounds; r++, s0 += NS) {
+#pragma unroll
+      for (int u = 0; u < NS; u++) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DMA * (NS - 2)));
+        asm volatile("s_barrier" ::: "memory");
+        dma(s0 + u + NS - 1, slots((u + NS - 1) % NS));
+        if constexpr (COMPUTE) compute_full(slots(u), acc);
+      }
+    }
+    for (; s0 < nst; s0 += NS) {
+#pragma unroll
+      for (int u = 0; u < NS; u++) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DMA * (NS - 2)));
+        asm volatile("s_barrier" ::: "memory");
+        dma(s0 + u + NS - 1, slots((u + NS - 1) % NS));
+        if constexpr (COMPUTE) compute(slots(u), steps_of(nsteps, s0 + u), acc);
+      }
+    }
+  }
+
+  template <typename Slots>
+  __device__ __forceinline__ void main_loop_dma(const Slots& slots, int64_t nst,
+                                                int64_t nsteps, bool computes,
+                                                f32x4_t (&acc)[CHAINS][FM][FN]) const {
+#pragma unroll
+    for (int u = 0; u < NS - 1; u++) dma(u, slots(u));
+    if (computes)
+      dma_rounds<true>(slots, nst, nsteps, acc);
+    else
+      dma_rounds<false>(slots, nst, nsteps, acc);
+  }
+
+  // Register-staged path (unaligned operands): two slots, double buffered.
+  template <typename Slots>
+  __device__ __forceinline__ void main_loop_slow(const Slots& slots, int64_t nst,
+                                                 int64_t nsteps, bool computes,
+                                                 f32x4_t (&acc)[CHAINS][FM][FN]) const {
+    uint4 ra[LA], rb[LB];
+    for (int64_t s = 0; s < nst; s++) {
+      gload_slow(s, ra, rb);
+      uint4* slot = (s & 1) ? slots(1) : slots(0);
+      sstore(slot, ra, rb);
+      __syncthreads();
+      if (computes) compute(slot, steps_of(nsteps, s), acc);
+      __syncthreads();
+    }
+  }
+};
+
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB>
+__global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
+  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB>;
+  constexpr int FM = Tile::FM, FN = Tile::FN, CHAINS = Tile::CHAINS, SC = Tile::STAGE_CH;
+  // The LDS ring: NS distinct arrays (unused ones are a single chunk).
+  __shared__ uint4 s0[SC], s1[SC];
+  __shared__ uint4 s2[NS > 2 ? SC : 1], s3[NS > 3 ? SC : 1], s4[NS > 4 ? SC : 1];
+  __shared__ uint4 s5[NS > 5 ? SC : 1], s6[NS > 6 ? SC : 1], s7[NS > 7 ? SC : 1];
+  // Slot u of the ring; u is a compile-time constant at every use (the loops
+  // over it are unrolled), so each access names one LDS array.
+  auto slots = [&](int u) -> uint4* {
+    switch (u) {
+      case 0: return s0;
+      case 1: return s1;
+      case 2: return s2;
+      case 3: return s3;
+      case 4: return s4;
+      case 5: return s5;
+      case 6: return s6;
+      default: return s7;
+    }
+  };
+
+  Tile t;
+  t.A = static_cast<const T*>(p.a);
+  t.B = static_cast<const T*>(p.b);
+  t.M = p.M;
+  t.N = p.N;
+  t.K = p.K;
+  t.tid = threadIdx.x;
+  t.lane = t.tid & 63;
+  t.wave = __builtin_amdgcn_readfirstlane(t.tid >> 6);
+  t.wm = (t.wave % Tile::CW) / WN;
+  t.wn = (t.wave % Tile::CW) % WN;
+  t.g = t.lane >> 4;
+  t.r16 = t.lane & 15;
+  const int tile = xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n);
+  t.m0 = (int64_t)(tile % p.tiles_m) * BM;
+  t.n0 = (int64_t)(tile / p.tiles_m) * BN;
+
+  const int64_t M = t.M, N = t.N, K = t.K;
+  const int64_t nst = (K + Tile::EPS - 1) / Tile::EPS;
+  // A chunk-step is 4 chunks of the row: 32 elements (16-bit) or 16 (fp32).
+  const int64_t nsteps = (K + 4 * Tile::EPC - 1) / (4 * Tile::EPC);
+  const int64_t wrow = t.m0 + t.wm * Tile::WTM, wcol = t.n0 + t.wn * Tile::WTN;
+  // Waves whose whole sub-tile lies outside C load but do not compute.
+  const bool computes = t.wave < Tile::CW && wrow < M && wcol < N;
+
+  f32x4_t acc[CHAINS][FM][FN];
+#pragma unroll
+  for (int ch = 0; ch < CHAINS; ch++)
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int jn = 0; jn < FN; jn++) acc[ch][i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  if (p.vec_a && p.vec_b) {
+    t.init_buffers();
+    t.init_dma();
+    t.main_loop_dma(slots, nst, nsteps, computes, acc);
+  } else {
+    t.main_loop_slow(slots, nst, nsteps, computes, acc);
+  }
+
+  if (!computes) return;
+  // Epilogue: one rounding per element.
+  T* __restrict__ out = static_cast<T*>(p.out);
+  const T* __restrict__ bias = static_cast<const T*>(p.bias);
+  const float alpha = p.alpha, beta = p.beta;
+#pragma unroll
+  for (int jn = 0; jn < FN; jn++) {
+    const int64_t col = wcol + jn * 16 + t.r16;
+    if (col >= N) continue;
+    const float bv = bias ? beta * Elem<T>::to_f32(bias[col]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int64_t row = wrow + i * 16 + 4 * t.g + e;
+        if (row < M) {
+          float v = acc[0][i][jn][e];
+          if constexpr (CHAINS == 2) v = v + acc[1][i][jn][e];
+          if (bias) v = __builtin_fmaf(alpha, v, bv);
+          out[row * N + col] = Elem<T>::from_f32(v);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ geometries
+
+// Footprints of C per workgroup. Every entry runs the same per-element
+// arithmetic; the table only trades parallelism against operand reuse and
+// latency hiding. Columns: id, BM, BN, WM, WN, NW (waves), KB (stage bytes),
+// NS (LDS ring stages).
+#define BI_GEOMETRIES(X)                  \
+  X(0, 16, 16, 1, 1, 4, 512, 6)           \
+  X(1, 64, 16, 4, 1, 4, 256, 4)           \
+  X(2, 64, 64, 2, 2, 4, 256, 3)           \
+  X(3, 128, 128, 4, 2, 8, 128, 4)         \
+  X(4, 256, 128, 4, 2, 8, 128, 3)
+
+using KernelFn = void (*)(GemmArgs);
+
+// Kernel for geometry g in the translation unit of element type T.
+template <typename T>
+KernelFn kernel_for(int g, bool trans_b) {
+#define BI_GEO_CASE(id, bm, bn, wm, wn, nw, kb, ns) \
+  case id: return trans_b ? gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true>  \
+                          : gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, false>;
+  switch (g) { BI_GEOMETRIES(BI_GEO_CASE) }
+#undef BI_GEO_CASE
+  return nullptr;
+}
+
+}  // namespace bi_gemm_dev
+
+// Per-type kernel tables, defined in bi_gemm_{f32,f16,bf16}.hip.
+bi_gemm_dev::KernelFn bi_gemm_kernel_f32(int g, bool trans_b);
+bi_gemm_dev::KernelFn bi_gemm_kernel_f16(int g, bool trans_b);
+bi_gemm_dev::KernelFn bi_gemm_kernel_bf16(int g, bool trans_b);

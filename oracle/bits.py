@@ -46,7 +46,8 @@ def round_f32_to(x, name):
     if name == "float32":
         return x.astype(np.float64)
     if name == "float16":
-        return x.astype(np.float16).astype(np.float64)
+        with np.errstate(over="ignore"):  # overflow rounds to +-inf, as intended
+            return x.astype(np.float16).astype(np.float64)
     if name == "bfloat16":
         u = x.view(np.uint32).astype(np.uint64)
         lsb = (u >> 16) & 1
@@ -64,5 +65,5 @@ def ulp_of(x, name):
     emin = {"float32": -126, "float16": -14, "bfloat16": -126}[name]
     ax = np.abs(np.asarray(x, dtype=np.float64))
     _, e = np.frexp(np.where(ax > 0, ax, 1.0))  # ax = m * 2**e, m in [0.5, 1)
-    e = np.maximum(e - 1, emin)
+    e = np.where(ax > 0, np.maximum(e - 1, emin), emin)
     return np.ldexp(1.0, (e - (p - 1)).astype(np.int64))

@@ -1,0 +1,307 @@
+"""Host-side logic, no GPU needed: the C ABI library loads and exports what
+include/*.h declares, rejects bad arguments before any HIP call, and the
+Python layer keeps the reference's validation, error types and routing-shim
+contract (reference tests/test_invariance.py:643-708, __init__.py:41-147,
+_gemm.py:185-208, _attention.py:173-239).
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import mlx_batch_invariant as bi
+from mlx_batch_invariant import _attention, _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = set()
+    for hdr in ("bi.h", "bi_testing.h"):
+        text = open(os.path.join(REPO, "include", hdr)).read()
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(bi_\w+)\s*\(", text, re.M))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    names = _declared_functions()
+    assert {"bi_gemm", "bi_sdpa", "bi_abi_version", "bi_last_error"} <= names
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for n in sorted(names):
+        assert hasattr(lib, n), n
+    assert set(_lib.SIGNATURES) == names
+
+
+def test_abi_version_and_geometry_table():
+    L = _lib.lib()
+    assert L.bi_abi_version() == _lib.ABI_VERSION == 1
+    geos = bi.geometries()
+    assert len(geos) == L.bi_gemm_num_geometries() >= 2
+    for bm, bn, w in geos:
+        assert bm % 16 == 0 and bn % 16 == 0 and w in (1, 2, 4, 8, 16)
+    assert L.bi_gemm_geometry_info(len(geos), None, None, None) == _lib.EINVAL
+    for M in (1, 16, 17, 64, 65, 256, 4096):
+        assert 0 <= L.bi_gemm_pick_geometry(M, 4096, 4096, _lib.BF16, 1) < len(geos)
+
+
+def _err():
+    return _lib.lib().bi_last_error().decode()
+
+
+def test_gemm_abi_rejects_bad_arguments_without_a_gpu():
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    args = lambda **kw: (kw.get("a", p), kw.get("b", p), None, kw.get("out", p), kw.get("M", 4),
+                         kw.get("N", 4), kw.get("K", 4), kw.get("dtype", _lib.BF16),
+                         kw.get("tb", 1), 1.0, 1.0, None)
+    assert L.bi_gemm(*args(dtype=7)) == _lib.EINVAL and "dtype" in _err()
+    assert L.bi_gemm(*args(M=-1)) == _lib.EINVAL and "negative" in _err()
+    assert L.bi_gemm(*args(tb=2)) == _lib.EINVAL
+    assert L.bi_gemm(*args(a=None)) == _lib.EINVAL and "null" in _err()
+    assert L.bi_gemm(*args(out=None)) == _lib.EINVAL
+    assert L.bi_gemm(*args(M=1 << 40)) == _lib.EINVAL
+    assert L.bi_gemm(*args(M=0)) == _lib.OK  # empty output: nothing to launch
+    assert L.bi_gemm(*args(N=0)) == _lib.OK
+    assert L.bi_gemm_with_geometry(*args()[:-1], 99, None) == _lib.EINVAL
+
+
+def test_sdpa_abi_rejects_bad_arguments_without_a_gpu():
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+
+    def call(B=1, H=8, Hkv=2, qL=1, N=16, D=128, V=128, mode=0, mask=None, dtype=_lib.BF16):
+        ms = _lib.i64_array([0, 0, 0]) if mask else None
+        return L.bi_sdpa(p, p, p, mask, ms, None, p, B, H, Hkv, qL, N, D, V, None, 0.1, mode, 0,
+                         dtype, None)
+
+    assert call(H=6, Hkv=4) == _lib.EINVAL and "multiple" in _err()
+    assert call(D=48, V=48) == _lib.EUNSUPPORTED and "head dims" in _err()
+    assert call(D=128, V=64) == _lib.EUNSUPPORTED
+    assert call(mode=5) == _lib.EINVAL
+    assert call(mode=2) == _lib.EINVAL and "mask" in _err()
+    assert call(dtype=9) == _lib.EINVAL
+    assert call(Hkv=0) == _lib.EINVAL
+    assert call(B=0) == _lib.OK and call(qL=0) == _lib.OK
+
+
+def test_status_codes_map_to_reference_exceptions():
+    L = _lib.lib()
+    L.bi_gemm(None, None, None, None, -1, 1, 1, 0, 0, 1.0, 1.0, None)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.EINVAL, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.EUNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.ELAUNCH, "x")
+    _lib.check(_lib.OK, "x")
+
+
+def test_tile_contract_is_pinned():
+    """Guard against anyone changing the per-element arithmetic (the analogue
+    of reference tests/test_invariance.py:468-470)."""
+    assert bi.TILE == dict(MFMA_16BIT="v_mfma_f32_16x16x32", MFMA_FP32="v_mfma_f32_16x16x4_f32",
+                           BK_BYTES=128, K_CHUNK_16BIT=32, K_CHUNK_FP32=16, FP32_CHAINS=2,
+                           EPILOGUE="fma(alpha, acc, beta * bias) then one RNE rounding")
+    assert _attention.PARTIALS == 32 and _attention.GROUP_LANES == 8
+    assert bi.HEAD_DIMS == (64, 128, 256)
+
+
+# ------------------------------------------------------------ Python validation
+
+def _t(*shape, dtype=torch.bfloat16):
+    return torch.zeros(*shape, dtype=dtype)
+
+
+def test_gemm_validation_matches_reference():
+    with pytest.raises(ValueError, match="share a dtype"):
+        bi.matmul(_t(2, 4), _t(4, 3, dtype=torch.float16))
+    with pytest.raises(ValueError, match="ndim"):
+        bi.matmul(_t(4), _t(4, 3))
+    with pytest.raises(ValueError, match="ndim"):
+        bi.matmul(_t(2, 4), _t(2, 4, 3))
+    with pytest.raises(ValueError, match="inner dimensions"):
+        bi.matmul(_t(2, 4), _t(5, 3))
+    with pytest.raises(ValueError, match="inner dimensions"):
+        bi.linear(_t(2, 4), _t(3, 5))
+    with pytest.raises(ValueError, match="bias must have shape"):
+        bi.addmm(_t(4), _t(2, 4), _t(4, 3))
+    with pytest.raises(ValueError, match="unsupported dtype"):
+        bi.matmul(_t(2, 4, dtype=torch.float64), _t(4, 3, dtype=torch.float64))
+    with pytest.raises(ValueError, match="GPU"):
+        bi.matmul(_t(2, 4), _t(4, 3))  # valid shapes, but CPU tensors: no fallback
+
+
+def test_sdpa_validation_matches_reference():
+    q, k, v = _t(1, 8, 2, 64), _t(1, 2, 16, 64), _t(1, 2, 16, 64)
+    with pytest.raises(ValueError, match="4-dimensional"):
+        bi.scaled_dot_product_attention(q[0], k, v)
+    with pytest.raises(ValueError, match="share a dtype"):
+        bi.scaled_dot_product_attention(q, k.float(), v)
+    with pytest.raises(ValueError, match="inconsistent"):
+        bi.scaled_dot_product_attention(q, k, _t(1, 2, 15, 64))
+    with pytest.raises(ValueError, match="multiple"):
+        bi.scaled_dot_product_attention(_t(1, 6, 2, 64), _t(1, 4, 16, 64), _t(1, 4, 16, 64))
+    with pytest.raises(ValueError, match="multiples of 32"):
+        bi.scaled_dot_product_attention(_t(1, 4, 1, 48), _t(1, 4, 8, 48), _t(1, 4, 8, 48))
+    with pytest.raises(NotImplementedError, match="not built"):
+        bi.scaled_dot_product_attention(_t(1, 4, 1, 96), _t(1, 4, 8, 96), _t(1, 4, 8, 96))
+    with pytest.raises(ValueError, match="sinks"):  # reference tests:355-364
+        bi.scaled_dot_product_attention(q, k, v, sinks=torch.zeros(4))
+    with pytest.raises(ValueError, match="causal"):
+        bi.scaled_dot_product_attention(q, k, v, mask="tril")
+    with pytest.raises(ValueError, match="broadcastable"):
+        bi.scaled_dot_product_attention(q, k, v, mask=torch.zeros(1, 1, 3, 16))
+    with pytest.raises(ValueError, match="GPU"):
+        bi.scaled_dot_product_attention(q, k, v)
+
+
+def test_mask_normalisation():
+    """Reference _attention.py:173-202: bool -> 0 / -inf in q's dtype, left-pad
+    to 4-D, zero strides on broadcast dimensions."""
+    m, strides, mode = _attention._mask_args(None, 2, 8, 3, 16, torch.bfloat16)
+    assert m is None and mode == _lib.MASK_NONE
+    _, _, mode = _attention._mask_args("causal", 2, 8, 3, 16, torch.bfloat16)
+    assert mode == _lib.MASK_CAUSAL
+    keep = torch.tensor([True, False] * 8)
+    m, strides, mode = _attention._mask_args(keep, 2, 8, 3, 16, torch.bfloat16)
+    assert mode == _lib.MASK_ARRAY and m.shape == (1, 1, 1, 16) and strides == (0, 0, 0)
+    assert m.dtype == torch.bfloat16 and m[0, 0, 0, 0] == 0 and m[0, 0, 0, 1] == float("-inf")
+    m, strides, _ = _attention._mask_args(torch.zeros(2, 1, 3, 16), 2, 8, 3, 16, torch.float16)
+    assert strides == (3 * 16, 0, 16) and m.dtype == torch.float16
+    m, strides, _ = _attention._mask_args(torch.zeros(8, 1, 16), 2, 8, 3, 16, torch.float16)
+    assert m.shape == (1, 8, 1, 16) and strides == (0, 16, 0)
+    with pytest.raises(ValueError):
+        _attention._mask_args(torch.zeros(1, 1, 1, 1, 16), 2, 8, 3, 16, torch.float16)
+
+
+# ----------------------------------------------------------------- routing shim
+
+class _Recorder:
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, name):
+        def fn(*args, **kwargs):
+            self.calls.append(name)
+            t = torch.zeros(1, 1)
+            t.routed_to = "bi:" + name
+            return t
+        return fn
+
+
+@pytest.fixture
+def stubbed(monkeypatch):
+    """Kernels replaced by recording stubs and every operand treated as
+    kernel-ready, so the shim's routing runs on the CPU (test-only)."""
+    rec = _Recorder()
+    monkeypatch.setattr(bi, "_kernel_ready", lambda *t: all(
+        x is None or (isinstance(x, torch.Tensor)
+                      and not (torch.is_grad_enabled() and x.requires_grad)) for x in t))
+    monkeypatch.setattr(bi, "matmul", rec("matmul"))
+    monkeypatch.setattr(bi, "addmm", rec("addmm"))
+    monkeypatch.setattr(bi, "linear", rec("linear"))
+    monkeypatch.setattr(bi, "_sdpa", rec("sdpa"))
+    return rec
+
+
+def test_shim_routes_supported_calls(stubbed):
+    a, w, c = torch.randn(3, 8), torch.randn(8, 5), torch.randn(5)
+    with bi.batch_invariant_mode(), torch.no_grad():
+        assert bi.is_enabled()
+        assert torch.matmul(a, w).routed_to == "bi:matmul"
+        assert (a @ w).routed_to == "bi:matmul"
+        assert a.matmul(w).routed_to == "bi:matmul"
+        assert torch.addmm(c, a, w).routed_to == "bi:addmm"
+        lin = torch.nn.Linear(8, 5)
+        assert lin(a).routed_to == "bi:linear"
+        assert F.linear(a, w.T).routed_to == "bi:linear"
+        n_lin = stubbed.calls.count("linear")
+        lin(torch.randn(8))  # 1-D input routed as a one-row batch
+        assert stubbed.calls.count("linear") == n_lin + 1
+        q, k = torch.randn(1, 8, 2, 64), torch.randn(1, 2, 16, 64)
+        assert F.scaled_dot_product_attention(q, k, k, enable_gqa=True).routed_to == "bi:sdpa"
+        y = F.scaled_dot_product_attention(q, k, k, is_causal=True, enable_gqa=True)
+        assert y.routed_to == "bi:sdpa"
+    assert not bi.is_enabled()
+    assert stubbed.calls.count("matmul") == 3 and "addmm" in stubbed.calls
+
+
+def test_strict_raises_and_non_strict_falls_back(stubbed):
+    """Reference tests:646-662: head dim 48 raises under strict and falls back
+    to stock otherwise."""
+    q, k = torch.randn(1, 4, 1, 48), torch.randn(1, 4, 8, 48)
+    stock = F.scaled_dot_product_attention(q, k, k, scale=0.1)
+    with bi.batch_invariant_mode(strict=True):
+        with pytest.raises(NotImplementedError, match="strict=False"):
+            F.scaled_dot_product_attention(q, k, k, scale=0.1)
+        with pytest.raises(NotImplementedError):
+            torch.matmul(torch.randn(4), torch.randn(4, 3))  # 1-D @ 2-D
+        with pytest.raises(NotImplementedError):
+            torch.addmm(torch.randn(3, 5), torch.randn(3, 8), torch.randn(8, 5))  # 2-D input
+        with pytest.raises(NotImplementedError):
+            F.scaled_dot_product_attention(torch.randn(1, 4, 2, 64), torch.randn(1, 4, 8, 64),
+                                           torch.randn(1, 4, 8, 64), dropout_p=0.1)
+        g = torch.randn(3, 8, requires_grad=True)
+        with pytest.raises(NotImplementedError):
+            torch.matmul(g, torch.randn(8, 5))  # autograd: the kernels have no backward
+    with bi.batch_invariant_mode(strict=False):
+        y = F.scaled_dot_product_attention(q, k, k, scale=0.1)
+    assert torch.equal(y, stock)
+
+
+def test_originals_restored_even_on_exception():
+    """Reference tests:686-698."""
+    before = (torch.matmul, torch.addmm, torch.Tensor.__matmul__, torch.Tensor.matmul,
+              torch.nn.Linear.forward, F.linear, F.scaled_dot_product_attention)
+    had = {n: n in vars(torch.Tensor) for n in ("__matmul__", "matmul")}
+    with pytest.raises(RuntimeError):
+        with bi.batch_invariant_mode():
+            assert bi.is_enabled()
+            raise RuntimeError("boom")
+    after = (torch.matmul, torch.addmm, torch.Tensor.__matmul__, torch.Tensor.matmul,
+             torch.nn.Linear.forward, F.linear, F.scaled_dot_product_attention)
+    assert before == after
+    assert {n: n in vars(torch.Tensor) for n in had} == had
+    assert not bi.is_enabled()
+
+
+def test_nesting_restores_only_at_outermost_exit():
+    """Reference tests:700-708."""
+    stock = torch.matmul
+    with bi.batch_invariant_mode():
+        patched = torch.matmul
+        assert patched is not stock
+        with bi.batch_invariant_mode():
+            assert torch.matmul is patched
+        assert torch.matmul is patched, "inner exit unpatched too early"
+    assert torch.matmul is stock
+
+
+def test_cpu_tensors_raise_under_strict_and_fall_back_otherwise():
+    a, w = torch.randn(3, 8), torch.randn(8, 5)
+    with bi.batch_invariant_mode(strict=True):
+        with pytest.raises(NotImplementedError):
+            torch.matmul(a, w)
+    with bi.batch_invariant_mode(strict=False):
+        assert torch.equal(torch.matmul(a, w), a @ w)
+
+
+# -------------------------------------------------------------- CLI and bench
+
+def test_cli_usage_exit_code(capsys):
+    from mlx_batch_invariant._cli import main
+
+    assert main([]) == 2
+    assert "usage: mlx-bi verify" in capsys.readouterr().err
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
