@@ -76,8 +76,8 @@ int bi_gemm(const void* a, const void* b, const void* bias, void* out,
             float alpha, float beta, void* hip_stream);
 
 /*
- * Single-pass scaled dot product attention, one workgroup per
- * (batch, head, query row).
+ * Single-pass scaled dot product attention; one workgroup owns the whole key
+ * reduction of a query row (for the query heads of one kv head together).
  *
  * Replaces the bi_sdpa launch `_KERNEL(inputs=[q, k, v, m, mstride, scale,
  * sinks], ...)` at reference mlx_batch_invariant/_attention.py:241-250 (kernel

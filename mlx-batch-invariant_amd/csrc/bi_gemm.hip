@@ -37,10 +37,12 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // largest footprint that still puts a workgroup on (nearly) every CU. The
 // thresholds come from measurements of this table on MI355X; since every
 // geometry computes the same bits, they only move time.
-int pick_geometry(int64_t M, int64_t N) {
+int pick_geometry(int64_t M, int64_t N, int dtype) {
   if (M <= 16) return 0;
   if (M <= 64) return 1;
-  if (ceil_div(M, 256) * ceil_div(N, 128) >= 200) return 4;
+  // fp32 carries two accumulator chains: the 256 x 128 footprint would need
+  // more than the 256 registers a wave of an 8-wave workgroup can hold.
+  if (dtype != BI_F32 && ceil_div(M, 256) * ceil_div(N, 128) >= 200) return 4;
   if (ceil_div(M, 128) * ceil_div(N, 128) >= 160) return 3;
   return 2;
 }
@@ -63,6 +65,25 @@ int validate(const void* a, const void* b, void* out, int64_t M, int64_t N, int6
   return BI_OK;
 }
 
+// 16-byte vector loads need 16-byte aligned bases and row lengths that are
+// multiples of a chunk (K for A and (N, K) B; N for (K, N) B). The buffer
+// path also needs every panel to fit a buffer resource (< 2 GiB).
+struct VecFlags {
+  bool a, b;
+};
+VecFlags vec_flags(const void* a, const void* b, int64_t N, int64_t K, int dtype, int trans_b,
+                   const Geometry& G) {
+  const int esz = bi::elem_size(dtype);
+  const int epc = 16 / esz;
+  const int64_t lim = (int64_t)1 << 31;
+  VecFlags v;
+  v.a = (K % epc == 0) && ((uintptr_t)a % 16 == 0) && (int64_t)G.bm * K * esz < lim;
+  v.b = (trans_b ? (K % epc == 0) && (int64_t)G.bn * K * esz < lim
+                 : (N % epc == 0) && K * N * esz < lim) &&
+        ((uintptr_t)b % 16 == 0);
+  return v;
+}
+
 int launch(const void* a, const void* b, const void* bias, void* out, int64_t M, int64_t N,
            int64_t K, int dtype, int trans_b, float alpha, float beta, int g, void* stream) {
   const Geometry& G = kGeometries[g];
@@ -78,19 +99,13 @@ int launch(const void* a, const void* b, const void* bias, void* out, int64_t M,
   p.tiles_n = (int)ceil_div(N, G.bn);
   p.alpha = alpha;
   p.beta = beta;
-  const int esz = bi::elem_size(dtype);
-  const int epc = 16 / esz;
-  // 16-byte vector loads need 16-byte aligned bases and row lengths that are
-  // multiples of a chunk (K for A and (N, K) B; N for (K, N) B).
-  // The buffer path also needs every panel to fit a buffer resource (< 2 GiB).
-  const int64_t lim = (int64_t)1 << 31;
-  p.vec_a = (K % epc == 0) && ((uintptr_t)a % 16 == 0) && (int64_t)G.bm * K * esz < lim;
-  p.vec_b = (trans_b ? (K % epc == 0) && (int64_t)G.bn * K * esz < lim
-                     : (N % epc == 0) && K * N * esz < lim) &&
-            ((uintptr_t)b % 16 == 0);
+  const VecFlags v = vec_flags(a, b, N, K, dtype, trans_b, G);
+  p.vec_a = v.a;
+  p.vec_b = v.b;
   const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
   if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_gemm: too many tiles");
   KernelFn fn = select_kernel(dtype, trans_b, g);
+  if (!fn) return bi::fail(BI_EUNSUPPORTED, "bi_gemm: geometry %d not built for this dtype", g);
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * G.waves), 0,
                      static_cast<hipStream_t>(stream), p);
   const hipError_t e = hipGetLastError();
@@ -105,7 +120,7 @@ extern "C" int bi_gemm(const void* a, const void* b, const void* bias, void* out
                        void* hip_stream) {
   const int rc = validate(a, b, out, M, N, K, dtype, trans_b);
   if (rc != BI_OK || M == 0 || N == 0) return rc;
-  return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta, pick_geometry(M, N),
+  return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta, pick_geometry(M, N, dtype),
                 hip_stream);
 }
 
@@ -121,9 +136,8 @@ extern "C" int bi_gemm_geometry_info(int g, int* block_m, int* block_n, int* wav
 
 extern "C" int bi_gemm_pick_geometry(int64_t M, int64_t N, int64_t K, int dtype, int trans_b) {
   (void)K;
-  (void)dtype;
   (void)trans_b;
-  return pick_geometry(M, N);
+  return pick_geometry(M, N, dtype);
 }
 
 extern "C" int bi_gemm_with_geometry(const void* a, const void* b, const void* bias, void* out,

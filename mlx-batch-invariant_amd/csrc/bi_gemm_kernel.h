@@ -165,6 +165,12 @@ constexpr int waitcnt_vm_lgkm0(int vm) {
 //       are in flight while one is computed. One barrier per stage.
 // The pipeline shape never changes what an output element computes: every
 // geometry issues the same chunk-steps in the same order (see file header).
+// One stage of the LDS ring: the A tile and the B tile, separate arrays.
+struct Slot {
+  uint4* a;
+  uint4* b;
+};
+
 template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB>
 struct GemmTile {
   static constexpr int NT = 64 * NW;
@@ -198,6 +204,26 @@ struct GemmTile {
   // (N, K) B, or columns n0.. of a (K, N) B); bytes past the valid rows are
   // outside num_records.
   __amdgpu_buffer_rsrc_t ra_src, rb_src;
+  // This lane's element offsets, within a stage's A and B arrays, of the
+  // operand chunk of chunk-step j for the wave's first 16-row (16-column)
+  // block; further blocks add 16 rows. Swizzles depend on the row mod 8 only,
+  // so they are the same for every block. The empty asm hides how the offsets
+  // were computed, which keeps each LDS read a short address chain off its
+  // array: the compiler then attributes every read to its ring slot and knows
+  // it does not depend on DMA still landing in other slots.
+  int a_off[CS], b_off[CS];
+
+  __device__ __forceinline__ void init_lds_offsets() {
+#pragma unroll
+    for (int j = 0; j < CS; j++) {
+      int ao = (wm * WTM + r16) * RC + ((4 * j + g) ^ swz_k(r16));
+      int bo = (wn * WTN + r16) * RC + ((4 * j + g) ^ swz_k(r16));
+      asm("" : "+v"(ao));
+      asm("" : "+v"(bo));
+      a_off[j] = ao;
+      b_off[j] = bo;
+    }
+  }
 
   __device__ __forceinline__ void init_buffers() {
     constexpr int64_t E = sizeof(T);
@@ -242,7 +268,7 @@ struct GemmTile {
   }
 
   // Issue this wave's LDS-DMA loads of stage s into `slot`.
-  __device__ __forceinline__ void dma(int64_t s, uint4* __restrict__ slot) const {
+  __device__ __forceinline__ void dma(int64_t s, Slot slot) const {
     constexpr uint32_t E = sizeof(T);
     const int32_t kleft = (int32_t)(K - s * EPS);  // K elements from this stage on
     const uint32_t a_step = (uint32_t)(s * EPS) * E;
@@ -250,7 +276,7 @@ struct GemmTile {
 #pragma unroll
     for (int i = 0; i < DMA; i++) {
       const bool is_a = i < DMA_A;
-      lds_void_t* dst = (lds_void_t*)(slot + (is_a ? 0 : A_CH) + dma_blk(i) * 64);
+      lds_void_t* dst = (lds_void_t*)((is_a ? slot.a : slot.b) + dma_blk(i) * 64);
       const uint32_t off = dma_kidx[i] < kleft ? dma_base[i] + (is_a ? a_step : b_step) : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? ra_src : rb_src, dst, 16, off, 0, 0, 0);
     }
@@ -277,8 +303,9 @@ struct GemmTile {
     }
   }
 
-  __device__ __forceinline__ void sstore(uint4* As, const uint4* ra, const uint4* rb) const {
-    uint4* Bs = As + A_CH;
+  __device__ __forceinline__ void sstore(Slot sl, const uint4* ra, const uint4* rb) const {
+    uint4* As = sl.a;
+    uint4* Bs = sl.b;
 #pragma unroll
     for (int i = 0; i < LA; i++) {
       const int q = tid + i * NT;
@@ -303,10 +330,9 @@ struct GemmTile {
   }
 
   // B operand chunk for chunk-step j of the 16-column block at tile column nb.
-  __device__ __forceinline__ uint4 load_b(const uint4* __restrict__ Bs, int j, int nb) const {
+  __device__ __forceinline__ uint4 load_b(const uint4* Bs, int j, int nb) const {
     if constexpr (TB) {
-      const int r = nb + r16;
-      return Bs[r * RC + ((4 * j + g) ^ swz_k(r))];
+      return Bs[b_off[j] + nb * RC];
     } else if constexpr (sizeof(T) == 2) {
       // ds_read_tr16_b64: in each 16-lane group, lane i receives element
       // (row 4t + i/4, column i%4) of the 16 x (4 x 16-bit) rows addressed by
@@ -316,7 +342,7 @@ struct GemmTile {
 #pragma unroll
       for (int half = 0; half < 2; half++) {
         const int kr = 32 * j + 8 * g + 4 * half + (r16 >> 2);
-        const int col = nb + 4 * (r16 & 3);
+        const int col = wn * WTN + nb + 4 * (r16 & 3);
         const int chunk = (col >> 3) ^ swz_nn<T, NN_CPR>(kr);
         const char* addr =
             reinterpret_cast<const char*>(Bs) + (kr * NN_CPR + chunk) * 16 + (col & 7) * 2;
@@ -331,7 +357,7 @@ struct GemmTile {
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const int kr = 16 * j + 4 * g + t;
-        const int col = nb + r16;
+        const int col = wn * WTN + nb + r16;
         const int chunk = (col >> 2) ^ swz_nn<T, NN_CPR>(kr);
         e[t] = __float_as_uint(Bf[(kr * NN_CPR + chunk) * 4 + (col & 3)]);
       }
@@ -339,21 +365,19 @@ struct GemmTile {
     }
   }
 
-  __device__ __forceinline__ void read_operands(const uint4* __restrict__ As, int j, uint4 (&av)[FM],
+  __device__ __forceinline__ void read_operands(Slot sl, int j, uint4 (&av)[FM],
                                                 uint4 (&bv)[FN]) const {
-    const uint4* Bs = As + A_CH;
+    const uint4* As = sl.a;
+    const uint4* Bs = sl.b;
 #pragma unroll
-    for (int i = 0; i < FM; i++) {
-      const int r = wm * WTM + i * 16 + r16;
-      av[i] = As[r * RC + ((4 * j + g) ^ swz_k(r))];
-    }
+    for (int i = 0; i < FM; i++) av[i] = As[a_off[j] + i * 16 * RC];
 #pragma unroll
-    for (int jn = 0; jn < FN; jn++) bv[jn] = load_b(Bs, j, wn * WTN + jn * 16);
+    for (int jn = 0; jn < FN; jn++) bv[jn] = load_b(Bs, j, jn * 16);
   }
 
   // All CS chunk-steps of the stage held in LDS at `As`, for every block of
   // this wave; operands of step j + 1 are read while step j's MFMAs run.
-  __device__ __forceinline__ void compute_full(const uint4* __restrict__ As,
+  __device__ __forceinline__ void compute_full(Slot As,
                                                f32x4_t (&acc)[CHAINS][FM][FN]) const {
     uint4 av[2][FM], bv[2][FN];
     read_operands(As, 0, av[0], bv[0]);
@@ -370,7 +394,7 @@ struct GemmTile {
   }
 
   // The first `steps` (< CS) chunk-steps of the last stage.
-  __device__ __forceinline__ void compute_part(const uint4* __restrict__ As, int steps,
+  __device__ __forceinline__ void compute_part(Slot As, int steps,
                                                f32x4_t (&acc)[CHAINS][FM][FN]) const {
 #pragma unroll
     for (int j = 0; j < CS - 1; j++) {
@@ -386,7 +410,7 @@ struct GemmTile {
     }
   }
 
-  __device__ __forceinline__ void compute(const uint4* __restrict__ As, int steps,
+  __device__ __forceinline__ void compute(Slot As, int steps,
                                           f32x4_t (&acc)[CHAINS][FM][FN]) const {
     if (steps == CS)
       compute_full(As, acc);
@@ -401,7 +425,11 @@ struct GemmTile {
 
   // Buffer path. The ring slots are distinct LDS arrays indexed at compile
   // time, which lets the compiler see that reading slot u does not depend on
-  // the DMA still landing in the other slots; the waits are explicit: before
+  // the DMA still landing in the other slots. That relies on the per-array
+  // alias scopes the compiler gives LDS accesses, so LDS pointers here carry
+  // no __restrict__ (its scopes would replace the per-array ones) and reads
+  // stay a short address chain off their array (see init_lds_offsets); either
+  // mistake makes every read wait for all DMA in flight. The waits are explicit: before
   // computing stage s, this wave's loads of stages s+1 .. s+NS-2 may still be
   // in flight, then a barrier makes every wave's part of stage s visible and
   // guarantees the slot about to be refilled is no longer read.
@@ -453,7 +481,7 @@ struct GemmTile {
     uint4 ra[LA], rb[LB];
     for (int64_t s = 0; s < nst; s++) {
       gload_slow(s, ra, rb);
-      uint4* slot = (s & 1) ? slots(1) : slots(0);
+      Slot slot = (s & 1) ? slots(1) : slots(0);
       sstore(slot, ra, rb);
       __syncthreads();
       if (computes) compute(slot, steps_of(nsteps, s), acc);
@@ -465,23 +493,25 @@ struct GemmTile {
 template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB>
 __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
   using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB>;
-  constexpr int FM = Tile::FM, FN = Tile::FN, CHAINS = Tile::CHAINS, SC = Tile::STAGE_CH;
-  // The LDS ring: NS distinct arrays (unused ones are a single chunk).
-  __shared__ uint4 s0[SC], s1[SC];
-  __shared__ uint4 s2[NS > 2 ? SC : 1], s3[NS > 3 ? SC : 1], s4[NS > 4 ? SC : 1];
-  __shared__ uint4 s5[NS > 5 ? SC : 1], s6[NS > 6 ? SC : 1], s7[NS > 7 ? SC : 1];
+  constexpr int FM = Tile::FM, FN = Tile::FN, CHAINS = Tile::CHAINS;
+  constexpr int AC = Tile::A_CH, BC = Tile::B_CH;
+  // The LDS ring: NS stages, each an A and a B array (unused ones are a single chunk).
+  __shared__ uint4 a0[AC], b0[BC], a1[AC], b1[BC];
+  __shared__ uint4 a2[NS > 2 ? AC : 1], b2[NS > 2 ? BC : 1], a3[NS > 3 ? AC : 1], b3[NS > 3 ? BC : 1];
+  __shared__ uint4 a4[NS > 4 ? AC : 1], b4[NS > 4 ? BC : 1], a5[NS > 5 ? AC : 1], b5[NS > 5 ? BC : 1];
+  __shared__ uint4 a6[NS > 6 ? AC : 1], b6[NS > 6 ? BC : 1], a7[NS > 7 ? AC : 1], b7[NS > 7 ? BC : 1];
   // Slot u of the ring; u is a compile-time constant at every use (the loops
   // over it are unrolled), so each access names one LDS array.
-  auto slots = [&](int u) -> uint4* {
+  auto slots = [&](int u) -> Slot {
     switch (u) {
-      case 0: return s0;
-      case 1: return s1;
-      case 2: return s2;
-      case 3: return s3;
-      case 4: return s4;
-      case 5: return s5;
-      case 6: return s6;
-      default: return s7;
+      case 0: return {a0, b0};
+      case 1: return {a1, b1};
+      case 2: return {a2, b2};
+      case 3: return {a3, b3};
+      case 4: return {a4, b4};
+      case 5: return {a5, b5};
+      case 6: return {a6, b6};
+      default: return {a7, b7};
     }
   };
 
@@ -518,6 +548,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int jn = 0; jn < FN; jn++) acc[ch][i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  t.init_lds_offsets();
   if (p.vec_a && p.vec_b) {
     t.init_buffers();
     t.init_dma();

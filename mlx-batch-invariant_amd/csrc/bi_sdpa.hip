@@ -1,11 +1,13 @@
 // Batch-invariant single-pass scaled dot product attention for gfx950.
 //
 // Restates the reference bi_sdpa (mlx_batch_invariant/_attention.py:32-149):
-// one workgroup per (batch, query head, query row) owns the whole reduction
-// over the key sequence; keys are split over a fixed number of partial online
-// softmaxes by key index; the partials are combined in a fixed order. There
-// is no split-KV, no second pass and no route switch on query length or
-// context length.
+// one workgroup owns the whole reduction over the key sequence for a query
+// row of a few heads (the query heads of one kv head that share its keys
+// under grouped-query attention); keys are split over a fixed number of
+// partial online softmaxes by key index; the partials are combined in a fixed
+// order. There is no split-KV, no second pass and no route switch on query
+// length or context length. How many heads share a workgroup changes only
+// which loads are shared, never a head's arithmetic.
 //
 // Fixed per-row arithmetic (the invariance contract):
 //   * 256 threads = 4 waves x 8 groups of 8 lanes = 32 partials. Key i belongs
@@ -77,24 +79,39 @@ __device__ inline int xcd_remap(int w, int total) {
   return w;
 }
 
+// This lane's 16-byte chunks r, r + 8, ... of a row of N_ELEM elements.
 template <typename T, int N_ELEM>
-__device__ inline void load_chunks(const T* __restrict__ row, int r, float* dst) {
+__device__ inline void load_raw(const T* __restrict__ row, int r, uint4* dst) {
   constexpr int CE = 16 / sizeof(T);
-  constexpr int NC = N_ELEM / CE / kGroupLanes;  // chunks per lane
+  constexpr int NC = N_ELEM / CE / kGroupLanes;
+#pragma unroll
+  for (int i = 0; i < NC; i++)
+    dst[i] = *reinterpret_cast<const uint4*>(row + (r + kGroupLanes * i) * CE);
+}
+
+template <typename T, int NC>
+__device__ inline void to_floats(const uint4* src, float* dst) {
+  constexpr int CE = 16 / sizeof(T);
 #pragma unroll
   for (int i = 0; i < NC; i++) {
-    const uint4 u = *reinterpret_cast<const uint4*>(row + (r + kGroupLanes * i) * CE);
-    const T* e = reinterpret_cast<const T*>(&u);
+    const T* e = reinterpret_cast<const T*>(&src[i]);
 #pragma unroll
     for (int t = 0; t < CE; t++) dst[i * CE + t] = to_f32<T>(e[t]);
   }
 }
 
-template <typename T, int D, int V>
+// One workgroup per (batch, kv head, group of GC query heads of that kv head,
+// query row). Every key and value row is loaded (and converted) once and used
+// by the GC heads, which share it under grouped-query attention; each head
+// keeps its own partial softmax state and runs exactly the per-row arithmetic
+// described above, so the result of a head does not depend on GC. The key
+// rows of the next PF keys of each partial are loaded ahead of their use.
+template <typename T, int D, int V, int GC, int PF>
 __global__ void __launch_bounds__(kThreads) sdpa_kernel(SdpaArgs p) {
   constexpr int CE = 16 / sizeof(T);
   constexpr int EQ = D / kGroupLanes;  // q/k elements per lane
   constexpr int EV = V / kGroupLanes;  // v/o elements per lane
+  constexpr int NCK = EQ / CE, NCV = EV / CE;  // 16-byte chunks per lane
   static_assert(D % (CE * kGroupLanes) == 0 && V % (CE * kGroupLanes) == 0, "head dim");
 
   __shared__ float part_m[kPartials], part_l[kPartials];
@@ -106,31 +123,39 @@ __global__ void __launch_bounds__(kThreads) sdpa_kernel(SdpaArgs p) {
   const int r = lane & 7;
 
   const int64_t G = p.H / p.Hkv;
-  int64_t t = xcd_remap(blockIdx.x, (int)(p.B * p.H * p.qL));
-  const int64_t hg = t % G;
-  t /= G;
+  const int64_t NHC = G / GC;  // head groups per kv head
+  int64_t t = xcd_remap(blockIdx.x, (int)(p.B * p.Hkv * NHC * p.qL));
+  const int64_t hc = t % NHC;
+  t /= NHC;
   const int64_t s = t % p.qL;
   t /= p.qL;
   const int64_t kvh = t % p.Hkv;
   const int64_t b = t / p.Hkv;
-  const int64_t h = kvh * G + hg;
+  const int64_t h0 = kvh * G + hc * GC;  // first query head of this workgroup
 
-  const T* __restrict__ qrow = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1] + s * p.qs[2];
   const T* __restrict__ kb = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
   const T* __restrict__ vb = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
 
-  float q2[EQ];
-  load_chunks<T, D>(qrow, r, q2);
+  float q2[GC][EQ];
+  float m[GC], l[GC];
+  float o[GC][EV];
 #pragma unroll
-  for (int e = 0; e < EQ; e++) q2[e] = q2[e] * p.scale2;
-
-  float m = -FLT_MAX, l = 0.f;
-  float o[EV];
+  for (int g = 0; g < GC; g++) {
+    const T* __restrict__ qrow =
+        static_cast<const T*>(p.q) + b * p.qs[0] + (h0 + g) * p.qs[1] + s * p.qs[2];
+    uint4 qc[NCK];
+    load_raw<T, D>(qrow, r, qc);
+    to_floats<T, NCK>(qc, q2[g]);
 #pragma unroll
-  for (int e = 0; e < EV; e++) o[e] = 0.f;
-  if (p.sinks && part == 0) {
-    m = to_f32<T>(static_cast<const T*>(p.sinks)[h]) * kLog2e;
-    l = 1.f;
+    for (int e = 0; e < EQ; e++) q2[g][e] = q2[g][e] * p.scale2;
+    m[g] = -FLT_MAX;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EV; e++) o[g][e] = 0.f;
+    if (p.sinks && part == 0) {
+      m[g] = to_f32<T>(static_cast<const T*>(p.sinks)[h0 + g]) * kLog2e;
+      l[g] = 1.f;
+    }
   }
 
   int64_t kend = p.N;
@@ -138,81 +163,136 @@ __global__ void __launch_bounds__(kThreads) sdpa_kernel(SdpaArgs p) {
     const int64_t last = s + p.causal_offset;  // last usable key
     kend = last < 0 ? 0 : (last + 1 < p.N ? last + 1 : p.N);
   }
-  const T* __restrict__ mrow = nullptr;
+  const T* __restrict__ mbase = nullptr;
   if (p.mask_mode == BI_MASK_ARRAY)
-    mrow = static_cast<const T*>(p.mask) + b * p.ms[0] + h * p.ms[1] + s * p.ms[2];
+    mbase = static_cast<const T*>(p.mask) + b * p.ms[0] + h0 * p.ms[1] + s * p.ms[2];
 
-  for (int64_t i = part; i < kend; i += kPartials) {
-    float bias2 = 0.f;
-    bool use = true;
-    if (mrow) {
-      const float mv = to_f32<T>(mrow[i]);
-      use = mv > -3.0e38f;
-      bias2 = mv * kLog2e;
+  // Key i of this partial: the raw chunks of the PF keys ahead live in kq/vq.
+  uint4 kq[PF][NCK], vq[PF][NCV];
+#pragma unroll
+  for (int u = 0; u < PF; u++) {
+    const int64_t i = part + (int64_t)kPartials * u;
+    if (i < kend) {
+      load_raw<T, D>(kb + i * p.ks[2], r, kq[u]);
+      load_raw<T, V>(vb + i * p.vs[2], r, vq[u]);
     }
-    if (use) {
-      float kf[EQ], vf[EV];
-      load_chunks<T, D>(kb + i * p.ks[2], r, kf);
-      load_chunks<T, V>(vb + i * p.vs[2], r, vf);
-      float d = 0.f;
+  }
+  for (int64_t i0 = part; i0 < kend; i0 += (int64_t)kPartials * PF) {
 #pragma unroll
-      for (int e = 0; e < EQ; e++) d = __builtin_fmaf(q2[e], kf[e], d);
-      const float sc = group_sum8(d) + bias2;
-      const float nm = fmaxf(m, sc);
-      const float f = __builtin_amdgcn_exp2f(m - nm);
-      const float pe = __builtin_amdgcn_exp2f(sc - nm);
-      m = nm;
-      l = __builtin_fmaf(l, f, pe);
+    for (int u = 0; u < PF; u++) {
+      const int64_t i = i0 + (int64_t)kPartials * u;
+      if (i < kend) {
+        float kf[EQ], vf[EV];
+        to_floats<T, NCK>(kq[u], kf);
+        to_floats<T, NCV>(vq[u], vf);
+        const int64_t inext = i + (int64_t)kPartials * PF;
+        if (inext < kend) {
+          load_raw<T, D>(kb + inext * p.ks[2], r, kq[u]);
+          load_raw<T, V>(vb + inext * p.vs[2], r, vq[u]);
+        }
 #pragma unroll
-      for (int e = 0; e < EV; e++) o[e] = __builtin_fmaf(pe, vf[e], o[e] * f);
+        for (int g = 0; g < GC; g++) {
+          float bias2 = 0.f;
+          bool use = true;
+          if (mbase) {
+            const float mv = to_f32<T>(mbase[g * p.ms[1] + i]);
+            use = mv > -3.0e38f;
+            bias2 = mv * kLog2e;
+          }
+          if (use) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < EQ; e++) d = __builtin_fmaf(q2[g][e], kf[e], d);
+            const float sc = group_sum8(d) + bias2;
+            const float nm = fmaxf(m[g], sc);
+            const float f = __builtin_amdgcn_exp2f(m[g] - nm);
+            const float pe = __builtin_amdgcn_exp2f(sc - nm);
+            m[g] = nm;
+            l[g] = __builtin_fmaf(l[g], f, pe);
+#pragma unroll
+            for (int e = 0; e < EV; e++) o[g][e] = __builtin_fmaf(pe, vf[e], o[g][e] * f);
+          }
+        }
+      }
     }
   }
 
-  // Fixed-order combine of the 32 partials.
-  if (r == 0) {
-    part_m[part] = m;
-    part_l[part] = l;
-  }
+  // Fixed-order combine of the 32 partials, one head at a time.
 #pragma unroll
-  for (int i = 0; i < EV / CE; i++)
-#pragma unroll
-    for (int e = 0; e < CE; e++) part_o[part * V + (r + kGroupLanes * i) * CE + e] = o[i * CE + e];
-  __syncthreads();
-
-  T* __restrict__ out = static_cast<T*>(p.out) + ((b * p.H + h) * p.qL + s) * V;
-  for (int e = tid; e < V; e += kThreads) {
-    float mx = part_m[0];
-#pragma unroll
-    for (int q = 1; q < kPartials; q++) mx = fmaxf(mx, part_m[q]);
-    float L = 0.f, acc = 0.f;
-#pragma unroll
-    for (int q = 0; q < kPartials; q++) {
-      const float f = __builtin_amdgcn_exp2f(part_m[q] - mx);
-      L = __builtin_fmaf(part_l[q], f, L);
-      acc = __builtin_fmaf(part_o[q * V + e], f, acc);
+  for (int g = 0; g < GC; g++) {
+    if (r == 0) {
+      part_m[part] = m[g];
+      part_l[part] = l[g];
     }
-    out[e] = from_f32<T>(L == 0.f ? acc : acc / L);
+#pragma unroll
+    for (int i = 0; i < EV / CE; i++)
+#pragma unroll
+      for (int e = 0; e < CE; e++)
+        part_o[part * V + (r + kGroupLanes * i) * CE + e] = o[g][i * CE + e];
+    __syncthreads();
+
+    T* __restrict__ out = static_cast<T*>(p.out) + ((b * p.H + h0 + g) * p.qL + s) * V;
+    for (int e = tid; e < V; e += kThreads) {
+      float mx = part_m[0];
+#pragma unroll
+      for (int q = 1; q < kPartials; q++) mx = fmaxf(mx, part_m[q]);
+      float L = 0.f, acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < kPartials; q++) {
+        const float f = __builtin_amdgcn_exp2f(part_m[q] - mx);
+        L = __builtin_fmaf(part_l[q], f, L);
+        acc = __builtin_fmaf(part_o[q * V + e], f, acc);
+      }
+      out[e] = from_f32<T>(L == 0.f ? acc : acc / L);
+    }
+    __syncthreads();
   }
 }
 
 using SdpaFn = void (*)(SdpaArgs);
 
-template <typename T>
-SdpaFn kernel_for_dims(int64_t D, int64_t V) {
-  if (D != V) return nullptr;
-  switch (D) {
-    case 64: return sdpa_kernel<T, 64, 64>;
-    case 128: return sdpa_kernel<T, 128, 128>;
-    case 256: return sdpa_kernel<T, 256, 256>;
+// Heads per workgroup: the largest supported count that divides the
+// query-head group; fewer for wide heads, whose per-head state (q and the
+// output accumulator) is larger.
+int heads_per_group(int64_t G, int64_t D) {
+  const int cap = D <= 64 ? 8 : (D <= 128 ? 4 : 2);
+  for (int gc = cap; gc > 1; gc >>= 1)
+    if (G % gc == 0) return gc;
+  return 1;
+}
+
+template <typename T, int D>
+SdpaFn kernel_for_group(int gc) {
+  constexpr int PF = 2;
+  switch (gc) {
+    case 1: return sdpa_kernel<T, D, D, 1, PF>;
+    case 2: return sdpa_kernel<T, D, D, 2, PF>;
+    case 4:
+      if constexpr (D <= 128) return sdpa_kernel<T, D, D, 4, PF>;
+      break;
+    case 8:
+      if constexpr (D <= 64) return sdpa_kernel<T, D, D, 8, PF>;
+      break;
   }
   return nullptr;
 }
 
-SdpaFn select_kernel(int dtype, int64_t D, int64_t V) {
+template <typename T>
+SdpaFn kernel_for_dims(int64_t D, int64_t V, int gc) {
+  if (D != V) return nullptr;
+  switch (D) {
+    case 64: return kernel_for_group<T, 64>(gc);
+    case 128: return kernel_for_group<T, 128>(gc);
+    case 256: return kernel_for_group<T, 256>(gc);
+  }
+  return nullptr;
+}
+
+SdpaFn select_kernel(int dtype, int64_t D, int64_t V, int gc) {
   switch (dtype) {
-    case BI_F32: return kernel_for_dims<float>(D, V);
-    case BI_F16: return kernel_for_dims<_Float16>(D, V);
-    case BI_BF16: return kernel_for_dims<__bf16>(D, V);
+    case BI_F32: return kernel_for_dims<float>(D, V, gc);
+    case BI_F16: return kernel_for_dims<_Float16>(D, V, gc);
+    case BI_BF16: return kernel_for_dims<__bf16>(D, V, gc);
   }
   return nullptr;
 }
@@ -236,13 +316,15 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
     return bi::fail(BI_EINVAL, "bi_sdpa: unknown mask mode %d", mask_mode);
   if (mask_mode == BI_MASK_ARRAY && (!mask || !mask_strides))
     return bi::fail(BI_EINVAL, "bi_sdpa: array mask needs a mask pointer and strides");
-  SdpaFn fn = select_kernel(dtype, D, V);
+  const int gc = heads_per_group(H / Hkv, D);
+  SdpaFn fn = select_kernel(dtype, D, V, gc);
   if (!fn)
     return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: head dims D=%lld V=%lld are not built "
                     "(supported: D == V in {64, 128, 256})", (long long)D, (long long)V);
   const int64_t rows = B * H * qL;
   if (rows == 0) return BI_OK;
   if (rows > INT32_MAX) return bi::fail(BI_EINVAL, "bi_sdpa: B*H*qL too large");
+  const int64_t blocks = rows / gc;
   if (!q || !out || (N > 0 && (!k || !v)))
     return bi::fail(BI_EINVAL, "bi_sdpa: null tensor pointer");
 
@@ -281,7 +363,7 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
   p.mask_mode = mask_mode;
   p.causal_offset = mask_mode == BI_MASK_CAUSAL ? causal_offset : 0;
 
-  hipLaunchKernelGGL(fn, dim3((unsigned)rows), dim3(kThreads), 0,
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), 0,
                      static_cast<hipStream_t>(hip_stream), p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return bi::launch_error(e, "bi_sdpa launch");

@@ -11,7 +11,6 @@ on the number of query rows, the batch, or how far the key sequence extends
 past the keys a row can see.
 """
 
-import ctypes
 import math
 
 import torch
@@ -85,16 +84,19 @@ def _sdpa(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks):
                               k.stride(0), k.stride(1), k.stride(2),
                               v.stride(0), v.stride(1), v.stride(2)])
     L = _lib.lib()
-    with torch.cuda.device(q.device):
-        rc = L.bi_sdpa(ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()),
-                       ctypes.c_void_p(v.data_ptr()),
-                       ctypes.c_void_p(mask.data_ptr() if mask is not None else None),
-                       _lib.i64_array(mstrides),
-                       ctypes.c_void_p(sinks.data_ptr() if sinks is not None else None),
-                       ctypes.c_void_p(out.data_ptr()),
-                       B, H, Hkv, qL, N, D, V, strides, float(scale), int(mask_mode),
-                       int(causal_offset), _lib.DTYPE_CODES[q.dtype], _lib.stream_of(q))
-    _lib.check(rc, "bi_sdpa")
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            mask.data_ptr() if mask is not None else None, _lib.i64_array(mstrides),
+            sinks.data_ptr() if sinks is not None else None, out.data_ptr(),
+            B, H, Hkv, qL, N, D, V, strides, float(scale), int(mask_mode),
+            int(causal_offset), _lib.DTYPE_CODES[q.dtype])
+    stream, switch = _lib.launch_stream(q.device)
+    if switch:
+        with torch.cuda.device(q.device):
+            rc = L.bi_sdpa(*args, stream)
+    else:
+        rc = L.bi_sdpa(*args, stream)
+    if rc:
+        _lib.check(rc, "bi_sdpa")
     return out
 
 

@@ -82,7 +82,7 @@ def _gemm(a, b, bias, transpose_b, alpha=1.0, beta=1.0, geometry=None):
     else:
         _check_device(a, b)
 
-    a2 = a.reshape(M, K)
+    a2 = a if len(lead) == 1 else a.reshape(M, K)
     if not a2.is_contiguous():
         a2 = a2.contiguous()
     # A (K, N) operand that is the transpose of a contiguous (N, K) tensor is
@@ -97,18 +97,24 @@ def _gemm(a, b, bias, transpose_b, alpha=1.0, beta=1.0, geometry=None):
     out = torch.empty((M, N), dtype=a.dtype, device=a.device)
     if M and N:
         L = _lib.lib()
-        args = (ctypes.c_void_p(a2.data_ptr()), ctypes.c_void_p(b.data_ptr()),
-                ctypes.c_void_p(bias_c.data_ptr() if bias_c is not None else None),
-                ctypes.c_void_p(out.data_ptr()), M, N, K, _lib.DTYPE_CODES[a.dtype],
-                int(transpose_b), float(alpha), float(beta))
-        with torch.cuda.device(a.device):
-            stream = _lib.stream_of(a)
-            if geometry is None:
-                rc = L.bi_gemm(*args, stream)
-            else:
-                rc = L.bi_gemm_with_geometry(*args, int(geometry), stream)
-        _lib.check(rc, "bi_gemm")
-    return out.reshape(*lead, N)
+        args = (a2.data_ptr(), b.data_ptr(), bias_c.data_ptr() if bias_c is not None else None,
+                out.data_ptr(), M, N, K, _lib.DTYPE_CODES[a.dtype], int(transpose_b),
+                float(alpha), float(beta))
+        stream, switch = _lib.launch_stream(a.device)
+        if switch:
+            with torch.cuda.device(a.device):
+                rc = _launch(L, args, geometry, stream)
+        else:
+            rc = _launch(L, args, geometry, stream)
+        if rc:
+            _lib.check(rc, "bi_gemm")
+    return out if len(lead) == 1 else out.reshape(*lead, N)
+
+
+def _launch(L, args, geometry, stream):
+    if geometry is None:
+        return L.bi_gemm(*args, stream)
+    return L.bi_gemm_with_geometry(*args, int(geometry), stream)
 
 
 def matmul(a, b):

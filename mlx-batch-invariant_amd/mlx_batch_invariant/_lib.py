@@ -83,9 +83,26 @@ def check(rc, what):
     raise RuntimeError("%s: %s" % (what, msg))
 
 
-def stream_of(t):
-    """Handle of torch's current HIP stream on t's device (graph-capture safe)."""
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def launch_stream(device):
+    """(stream handle as int, needs_device_switch) for a launch on `device`.
+
+    The raw handle of torch's current stream, read without building a Stream
+    object (the launch path is host-bound for small problems). A launch on a
+    device other than the current one runs under torch.cuda.device: the null
+    (default) stream always means the current device to HIP.
+    """
+    idx = device.index
+    cur = torch.cuda.current_device()
+    if idx is None:
+        idx = cur
+    if _raw_stream is not None:
+        handle = _raw_stream(idx)
+    else:
+        handle = torch.cuda.current_stream(idx).cuda_stream
+    return handle, idx != cur
 
 
 def i64_array(values):

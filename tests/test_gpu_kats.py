@@ -28,8 +28,11 @@ def test_gemm_kats(cuda, i):
         b = torch.tensor(case["b"], dtype=dtype, device=cuda)
         c = None if case["bias"] is None else torch.tensor(case["bias"], dtype=dtype, device=cuda)
         for g in range(len(_gemm.geometries())):
-            got = f64(_gemm._gemm(a, b, c, case["trans_b"], case["alpha"], case["beta"], geometry=g))
-            assert (got == want).all(), (dname, g)
+            try:
+                y = _gemm._gemm(a, b, c, case["trans_b"], case["alpha"], case["beta"], geometry=g)
+            except NotImplementedError:
+                continue  # geometry built for 16-bit, aligned operands only
+            assert (f64(y) == want).all(), (dname, g)
 
 
 @pytest.mark.parametrize("i", range(len(KATS["sdpa"])))
