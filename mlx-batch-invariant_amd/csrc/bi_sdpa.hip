@@ -30,6 +30,7 @@
 //     out = L == 0 ? o : o / L (reference :124-141), one rounding to T.
 #include <hip/hip_runtime.h>
 #include <float.h>
+#include <atomic>
 #include <stdint.h>
 
 #include "bi_internal.h"
@@ -254,10 +255,31 @@ using SdpaFn = void (*)(SdpaArgs);
 // Heads per workgroup: the largest supported count that divides the
 // query-head group; fewer for wide heads, whose per-head state (q and the
 // output accumulator) is larger.
-int heads_per_group(int64_t G, int64_t D) {
+// Compute units of the current device, read once per device.
+int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Heads per workgroup: the largest supported count that divides the
+// query-head group and still leaves about two workgroups per compute unit
+// (`rows` query rows in all); fewer for wide heads, whose per-head state (q
+// and the output accumulator) is larger. The choice only decides which loads
+// are shared.
+int heads_per_group(int64_t G, int64_t D, int64_t rows) {
   const int cap = D <= 64 ? 8 : (D <= 128 ? 4 : 2);
+  const int64_t want = 2 * (int64_t)device_cus();
   for (int gc = cap; gc > 1; gc >>= 1)
-    if (G % gc == 0) return gc;
+    if (G % gc == 0 && rows / gc >= want) return gc;
   return 1;
 }
 
@@ -316,14 +338,14 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
     return bi::fail(BI_EINVAL, "bi_sdpa: unknown mask mode %d", mask_mode);
   if (mask_mode == BI_MASK_ARRAY && (!mask || !mask_strides))
     return bi::fail(BI_EINVAL, "bi_sdpa: array mask needs a mask pointer and strides");
-  const int gc = heads_per_group(H / Hkv, D);
-  SdpaFn fn = select_kernel(dtype, D, V, gc);
-  if (!fn)
+  if (!select_kernel(dtype, D, V, 1))
     return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: head dims D=%lld V=%lld are not built "
                     "(supported: D == V in {64, 128, 256})", (long long)D, (long long)V);
   const int64_t rows = B * H * qL;
   if (rows == 0) return BI_OK;
   if (rows > INT32_MAX) return bi::fail(BI_EINVAL, "bi_sdpa: B*H*qL too large");
+  const int gc = heads_per_group(H / Hkv, D, rows);
+  SdpaFn fn = select_kernel(dtype, D, V, gc);
   const int64_t blocks = rows / gc;
   if (!q || !out || (N > 0 && (!k || !v)))
     return bi::fail(BI_EINVAL, "bi_sdpa: null tensor pointer");

@@ -74,6 +74,29 @@ def test_batch_invariance(cuda):
                     assert int((got != base).sum()) == 0, "sdpa %s B=%d idx=%d" % (dname, B, idx)
 
 
+@pytest.mark.parametrize("H,Hkv,D,batches", [(32, 8, 128, (1, 32, 64)),
+                                              (32, 4, 64, (1, 32, 64, 128))])
+def test_head_grouping_does_not_change_bits(cuda, H, Hkv, D, batches):
+    """Large grids let one workgroup serve several query heads of a GQA group
+    (sharing their key and value loads); small grids give each head its own
+    workgroup. The batch sizes here cross both choices: a row's bits must not
+    move."""
+    N = 256
+    for dname, dtype in DTYPES:
+        q1 = rn((1, H, 1, D), dtype, 31, device=cuda)
+        k1, v1 = rn((1, Hkv, N, D), dtype, 32, device=cuda), rn((1, Hkv, N, D), dtype, 33, device=cuda)
+        B = max(batches)
+        qp = rn((B, H, 1, D), dtype, 34, device=cuda)
+        kp, vp = rn((B, Hkv, N, D), dtype, 35, device=cuda), rn((B, Hkv, N, D), dtype, 36, device=cuda)
+        base = bits(bi.scaled_dot_product_attention(q1, k1, v1, mask="causal")[0])
+        for B in batches[1:]:
+            idx = B - 1
+            y = bi.scaled_dot_product_attention(batch_with(q1, qp, B, idx), batch_with(k1, kp, B, idx),
+                                                batch_with(v1, vp, B, idx), mask="causal")
+            assert int((bits(y[idx]) != base).sum()) == 0, "%s H=%d Hkv=%d D=%d B=%d" % (
+                dname, H, Hkv, D, B)
+
+
 def test_causal_and_masks_are_invariant(cuda):
     H, Hkv, N, D = 8, 4, 1024, 128
     for dname, dtype in DTYPES:
