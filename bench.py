@@ -106,12 +106,44 @@ def cpu_baseline(ops):
                       "(oracle/csrc/oracle.c), %.1f s" % (passes, CPU_ROWS, M, dt)}
 
 
+def model_determinism(torch, bi, dev):
+    """random-init 32-layer Llama-shaped decoder, 512-token seeded
+    prompt; bits of sequence 0's last-position logits at batch 8 vs batch 1,
+    under batch_invariant_mode and stock; and the prefill time of both paths
+    at batch 8 (HIP events, median of 3)."""
+    from mlx_batch_invariant import decoder
+
+    m = decoder.build(decoder.LLAMA_7B_SHAPE, device=dev, seed=0)
+    ids = decoder.prompts(m.c, 8, 512, seed=0, device=dev)
+    out = {"config": "configs[5]: %d layers, hidden %d, %d/%d heads, FFN %d, vocab %d, bf16, "
+                     "512-token prompt; sequence 0 at batch 8 vs batch 1"
+                     % (m.c.layers, m.c.hidden, m.c.heads, m.c.kv_heads, m.c.inter, m.c.vocab)}
+    for label, inv in (("invariant", True), ("stock", False)):
+        base = decoder.logits_bits(m, ids[:1], inv)
+        out["%s_bits_differing" % label] = int((decoder.logits_bits(m, ids, inv) != base).sum())
+        times = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            decoder.logits_bits(m, ids, inv)
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        out["%s_prefill_ms_batch8" % label] = round(statistics.median(times), 2)
+    out["logits"] = m.c.vocab
+    del m
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the 32-layer decoder determinism check (configs[5])")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy three times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -234,6 +266,7 @@ def main():
     for b in (2, 3, 8, 16, 33, 64, 128, 256):
         differing += int((bits(bi.matmul(a[:b].contiguous(), w)[0]) != ref).sum())
 
+    model = None if args.no_model else model_determinism(torch, bi, dev)
     cpu = None if args.no_cpu else cpu_baseline(ops)
 
     line = {
@@ -248,6 +281,7 @@ def main():
         "per_shape": per_shape,
         "sdpa_decode": sdpa,
         "invariance_bits_differing_batch_1_to_256": differing,
+        "model_determinism": model,
         "device": torch.cuda.get_device_name(0),
     }
     print(json.dumps(line))

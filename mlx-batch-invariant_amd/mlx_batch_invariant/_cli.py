@@ -16,6 +16,7 @@ from . import __version__, scaled_dot_product_attention
 from ._gemm import linear
 
 _DTYPES = ("bfloat16", "float16", "float32")
+_FULL_BATCHES = [1, 2, 3, 5, 8, 16, 31, 32, 33, 64, 128, 256]
 
 
 def _bits(t):
@@ -140,6 +141,9 @@ def verify(argv=None):
                    help="repeatable; default is all three")
     p.add_argument("--quick", action="store_true", help="one shape per op")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--model", action="store_true",
+                   help="also run the 32-layer synthetic decoder: sequence 0's logits at "
+                        "batch 2/4/8 vs batch 1 (needs ~12 GB of device memory)")
     args = p.parse_args(argv)
 
     import torch
@@ -151,7 +155,7 @@ def verify(argv=None):
     device = torch.device("cuda:0")
     gen = torch.Generator().manual_seed(args.seed)
     dtypes = [getattr(torch, d) for d in (args.dtype or _DTYPES)]
-    batches = [1, 2, 8, 32] if args.quick else [1, 2, 3, 5, 8, 16, 31, 32, 33, 64, 128, 256]
+    batches = [1, 2, 8, 32] if args.quick else _FULL_BATCHES
     qLs = [1, 2, 8, 9] if args.quick else [1, 2, 3, 4, 7, 8, 9, 16, 17]
     gemms = [(4096, 4096)] if args.quick else [(512, 1024), (4096, 4096), (11008, 4096)]
     attns = [(8, 8, 1024, 128)] if args.quick else [
@@ -186,8 +190,26 @@ def verify(argv=None):
         print("  %-9s linear   hipGraph replay            %s"
               % (name, "ok" if not bad else "VARIANT at replay %s" % bad))
 
+    if args.model:
+        from . import decoder
+
+        m = decoder.build(decoder.LLAMA_7B_SHAPE, device=device, seed=args.seed)
+        got = decoder.determinism(m, length=512, batches=(2, 4, 8), seed=args.seed)
+        stock = decoder.determinism(m, length=512, batches=(2, 4, 8), seed=args.seed,
+                                    invariant=False)
+        del m
+        torch.cuda.empty_cache()
+        bad = {B: d for B, d in got.items() if d}
+        fails += bool(bad)
+        print("  decoder  %d layers, 512-token prompt: %s  (stock: %s of %d logits differ)"
+              % (decoder.LLAMA_7B_SHAPE.layers,
+                 "ok" if not bad else "VARIANT logits at batch %s" % bad,
+                 "/".join(str(stock[B]) for B in sorted(stock)), decoder.LLAMA_7B_SHAPE.vocab))
+
     # A suite that cannot fail proves nothing: confirm stock torch is still variant.
-    stock = _stock_matmul_variant(batches, gen, device)
+    # The control always sweeps the full batch list: hipBLASLt switches kernels
+    # at sizes the quick list may not reach.
+    stock = _stock_matmul_variant(_FULL_BATCHES, gen, device)
     print("\ncontrol: stock torch.matmul -> %s"
           % ("VARIANT at %s (expected)" % stock[0] if stock
              else "invariant on every swept shape -- this check is no longer proving anything"))
@@ -202,7 +224,7 @@ def main(argv=None):
     argv = list(sys.argv[1:] if argv is None else argv)
     if argv and argv[0] == "verify":
         return verify(argv[1:])
-    print("usage: mlx-bi verify [--quick] [--dtype float32|float16|bfloat16] [--seed N]",
+    print("usage: mlx-bi verify [--quick] [--dtype float32|float16|bfloat16] [--seed N] [--model]",
           file=sys.stderr)
     return 2
 

@@ -305,3 +305,22 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_decoder_harness_on_cpu():
+    """The synthetic decoder builds and runs on the CPU (stock ops only: the
+    invariant kernels need the GPU); prompts and weights follow their seeds."""
+    from mlx_batch_invariant import decoder
+
+    c = decoder.DecoderConfig(hidden=64, inter=128, heads=4, kv_heads=2, head_dim=16,
+                              layers=2, vocab=100)
+    m1 = decoder.build(c, device="cpu", dtype=torch.float32, seed=3)
+    m2 = decoder.build(c, device="cpu", dtype=torch.float32, seed=3)
+    assert all(torch.equal(a, b) for a, b in zip(m1.parameters(), m2.parameters()))
+    ids = decoder.prompts(c, 4, 10, seed=1, device="cpu")
+    assert ids.shape == (4, 10) and torch.equal(ids, decoder.prompts(c, 4, 10, seed=1, device="cpu"))
+    with torch.no_grad():
+        y = m1(ids)
+    assert y.shape == (4, c.vocab) and torch.isfinite(y).all()
+    got = decoder.determinism(m1, length=10, batches=(2, 4), seed=1, invariant=False)
+    assert set(got) == {2, 4} and all(v >= 0 for v in got.values())
