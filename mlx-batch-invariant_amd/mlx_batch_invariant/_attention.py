@@ -72,7 +72,19 @@ def _kernel_view(t):
 
 
 def _sdpa(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks):
-    """Launch after validation: q (B,H,qL,D), k (B,Hkv,N,D), v (B,Hkv,N,V)."""
+    """Launch after validation: q (B,H,qL,D), k (B,Hkv,N,D), v (B,Hkv,N,V).
+    While torch.compile traces, the launch is recorded as the opaque op
+    mlx_bi::sdpa."""
+    if torch.compiler.is_compiling():
+        from . import _ops  # noqa: F401  (registers the ops)
+
+        return torch.ops.mlx_bi.sdpa(q, k, v, float(scale), int(mask_mode), mask,
+                                     [int(x) if isinstance(x, int) else x for x in mstrides],
+                                     int(causal_offset), sinks)
+    return _sdpa_eager(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks)
+
+
+def _sdpa_eager(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks):
     B, H, qL, D = q.shape
     _, Hkv, N, _ = k.shape
     V = v.shape[-1]

@@ -56,7 +56,16 @@ def _check_device(*tensors):
 
 
 def _gemm(a, b, bias, transpose_b, alpha=1.0, beta=1.0, geometry=None):
-    """Validation and launch; reference _gemm.py:185-222."""
+    """Validation and launch; reference _gemm.py:185-222. While torch.compile
+    traces, the launch is recorded as the opaque op mlx_bi::gemm."""
+    if geometry is None and torch.compiler.is_compiling():
+        from . import _ops  # noqa: F401  (registers the ops)
+
+        return torch.ops.mlx_bi.gemm(a, b, bias, bool(transpose_b), float(alpha), float(beta))
+    return _gemm_eager(a, b, bias, transpose_b, alpha, beta, geometry)
+
+
+def _gemm_eager(a, b, bias, transpose_b, alpha=1.0, beta=1.0, geometry=None):
     if a.dtype != b.dtype:
         raise ValueError("a and b must share a dtype, got %s and %s" % (a.dtype, b.dtype))
     if a.ndim < 2 or b.ndim != 2:

@@ -324,3 +324,21 @@ def test_decoder_harness_on_cpu():
     assert y.shape == (4, c.vocab) and torch.isfinite(y).all()
     got = decoder.determinism(m1, length=10, batches=(2, 4), seed=1, invariant=False)
     assert set(got) == {2, 4} and all(v >= 0 for v in got.values())
+
+
+def test_custom_op_fake_shapes():
+    """torch.compile sees bi.* calls as the opaque ops mlx_bi::gemm / mlx_bi::sdpa;
+    their fake implementations give the output shapes without a GPU."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from mlx_batch_invariant import _ops
+
+    with FakeTensorMode():
+        a = torch.empty(3, 5, 64, dtype=torch.bfloat16)
+        assert _ops.gemm(a, torch.empty(96, 64, dtype=torch.bfloat16), None, True, 1.0,
+                         1.0).shape == (3, 5, 96)
+        assert _ops.gemm(a, torch.empty(64, 80, dtype=torch.bfloat16), None, False, 1.0,
+                         1.0).shape == (3, 5, 80)
+        q, k = torch.empty(2, 8, 3, 64), torch.empty(2, 2, 10, 64)
+        assert _ops.sdpa(q, k, torch.empty(2, 2, 10, 32), 0.1, 0, None, [0, 0, 0], 0,
+                         None).shape == (2, 8, 3, 32)
