@@ -111,6 +111,31 @@ int bi_sdpa(const void* q, const void* k, const void* v,
             float scale, int mask_mode, int64_t causal_offset,
             int dtype, void* hip_stream);
 
+/*
+ * out = x @ dequantize(w).T for an affine-quantized weight, without
+ * materialising the dequantized matrix.
+ *
+ * Replaces the bi_qgemm launch `_QKERNEL(inputs=[x, w, scales, qbias, ...])`
+ * at reference mlx_batch_invariant/_gemm.py:275-284 (quantized_linear
+ * :243-285; the kernel's dequantizing B load :163-177).
+ *
+ *   x       (M, K) row-major, dtype BI_F16 or BI_BF16, 16-byte aligned
+ *   w       (N, K * bits / 32) uint32, 16-byte aligned: weight element k of
+ *           row n is bits bits * (k % (32 / bits)) .. of word k / (32 / bits)
+ *           of that row (little-endian packing, the MLX affine layout)
+ *   scales, (N, K / group_size) in the element type of x; element k of row n
+ *   biases  dequantizes to T(fp32(scales[n][k/group] * q + biases[n][k/group]))
+ *   out     (M, N) row-major
+ *   bits in {2, 4, 8}; group_size in {32, 64, 128} and dividing K.
+ *
+ * The result is bitwise that of bi_gemm (trans_b = 1, no bias) on the
+ * dequantized weight, with the same invariance: nothing depends on M or on a
+ * row's batch neighbours. BI_F32 activations return BI_EUNSUPPORTED.
+ */
+int bi_qgemm(const void* x, const void* w, const void* scales, const void* biases, void* out,
+             int64_t M, int64_t N, int64_t K, int group_size, int bits, int dtype,
+             void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,11 @@ int bi_gemm_with_geometry(const void* a, const void* b, const void* bias, void* 
                           int64_t M, int64_t N, int64_t K, int dtype, int trans_b,
                           float alpha, float beta, int g, void* hip_stream);
 
+/* bi_qgemm with the geometry forced to `g` (same arguments and semantics). */
+int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
+                           const void* biases, void* out, int64_t M, int64_t N, int64_t K,
+                           int group_size, int bits, int dtype, int g, void* hip_stream);
+
 /* Wavefront width the kernels were compiled for (64 on gfx950); the fixed
  * reduction shapes assume it. Reads a device-side constant: needs a GPU. */
 int bi_device_wavefront_size(int* out);

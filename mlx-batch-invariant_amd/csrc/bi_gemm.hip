@@ -149,6 +149,115 @@ extern "C" int bi_gemm_with_geometry(const void* a, const void* b, const void* b
   return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta, g, hip_stream);
 }
 
+// ------------------------------------------------------------------ quantized
+
+namespace {
+
+KernelFn select_qkernel(int dtype, int g, int bits) {
+  switch (dtype) {
+    case BI_F16: return bi_qgemm_kernel_f16(g, bits);
+    case BI_BF16: return bi_qgemm_kernel_bf16(g, bits);
+  }
+  return nullptr;
+}
+
+int group_shift(int group_size) {
+  switch (group_size) {
+    case 32: return 5;
+    case 64: return 6;
+    case 128: return 7;
+  }
+  return -1;
+}
+
+int qvalidate(const void* x, const void* w, const void* scales, const void* biases, void* out,
+              int64_t M, int64_t N, int64_t K, int group_size, int bits, int dtype) {
+  if (dtype != BI_F32 && dtype != BI_F16 && dtype != BI_BF16)
+    return bi::fail(BI_EINVAL, "bi_qgemm: unknown dtype %d", dtype);
+  if (bits != 2 && bits != 4 && bits != 8)
+    return bi::fail(BI_EINVAL, "bi_qgemm: bits must be one of (2, 4, 8), got %d", bits);
+  if (group_shift(group_size) < 0)
+    return bi::fail(BI_EINVAL, "bi_qgemm: group size must be 32, 64 or 128, got %d", group_size);
+  if (M < 0 || N < 0 || K < 0)
+    return bi::fail(BI_EINVAL, "bi_qgemm: negative size M=%lld N=%lld K=%lld", (long long)M,
+                    (long long)N, (long long)K);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return bi::fail(BI_EINVAL, "bi_qgemm: dimension too large");
+  if (K % group_size)
+    return bi::fail(BI_EINVAL, "bi_qgemm: group size %d does not divide K=%lld", group_size,
+                    (long long)K);
+  if (dtype == BI_F32)
+    return bi::fail(BI_EUNSUPPORTED,
+                    "bi_qgemm: quantized weights are built for float16/bfloat16 activations");
+  if (M == 0 || N == 0) return BI_OK;
+  if (!out || (K > 0 && (!x || !w || !scales || !biases)))
+    return bi::fail(BI_EINVAL, "bi_qgemm: null operand pointer");
+  if ((uintptr_t)x % 16 || (uintptr_t)w % 16 || (uintptr_t)scales % 2 || (uintptr_t)biases % 2)
+    return bi::fail(BI_EINVAL, "bi_qgemm: x and the packed weight must be 16-byte aligned");
+  const int64_t tiles = ceil_div(M, 16) * ceil_div(N, 16);
+  if (tiles > INT32_MAX) return bi::fail(BI_EINVAL, "bi_qgemm: output too large");
+  return BI_OK;
+}
+
+int qlaunch(const void* x, const void* w, const void* scales, const void* biases, void* out,
+            int64_t M, int64_t N, int64_t K, int group_size, int bits, int dtype, int g,
+            void* stream) {
+  const Geometry& G = kGeometries[g];
+  const int64_t lim = (int64_t)1 << 31;
+  if ((int64_t)G.bm * K * 2 >= lim || (int64_t)G.bn * K * bits / 8 >= lim)
+    return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: operand panel of 2 GiB or more");
+  GemmArgs p = {};
+  p.a = x;
+  p.b = w;
+  p.bias = nullptr;
+  p.out = out;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.tiles_m = (int)ceil_div(M, G.bm);
+  p.tiles_n = (int)ceil_div(N, G.bn);
+  p.alpha = 1.f;
+  p.beta = 1.f;
+  p.vec_a = 1;
+  p.vec_b = 1;
+  p.qs = scales;
+  p.qz = biases;
+  p.qgroup_shift = group_shift(group_size);
+  const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
+  if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_qgemm: too many tiles");
+  KernelFn fn = select_qkernel(dtype, g, bits);
+  if (!fn) return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: geometry %d not built", g);
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * G.waves), 0,
+                     static_cast<hipStream_t>(stream), p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return bi::launch_error(e, "bi_qgemm launch");
+  return BI_OK;
+}
+
+}  // namespace
+
+extern "C" int bi_qgemm(const void* x, const void* w, const void* scales, const void* biases,
+                        void* out, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                        int dtype, void* hip_stream) {
+  const int rc = qvalidate(x, w, scales, biases, out, M, N, K, group_size, bits, dtype);
+  if (rc != BI_OK || M == 0 || N == 0) return rc;
+  // The 256 x 128 footprint needs more registers with the dequantizing
+  // loads in flight; 128 x 128 takes its place.
+  int g = pick_geometry(M, N, dtype);
+  if (g == 4) g = 3;
+  return qlaunch(x, w, scales, biases, out, M, N, K, group_size, bits, dtype, g, hip_stream);
+}
+
+extern "C" int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
+                                      const void* biases, void* out, int64_t M, int64_t N,
+                                      int64_t K, int group_size, int bits, int dtype, int g,
+                                      void* hip_stream) {
+  if (g < 0 || g >= kNumGeometries) return bi::fail(BI_EINVAL, "unknown geometry %d", g);
+  const int rc = qvalidate(x, w, scales, biases, out, M, N, K, group_size, bits, dtype);
+  if (rc != BI_OK || M == 0 || N == 0) return rc;
+  return qlaunch(x, w, scales, biases, out, M, N, K, group_size, bits, dtype, g, hip_stream);
+}
+
 namespace {
 __global__ void wavefront_size_kernel(int* out) {
   if (threadIdx.x == 0) out[0] = __builtin_amdgcn_wavefrontsize();

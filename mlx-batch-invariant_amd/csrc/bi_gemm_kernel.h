@@ -53,6 +53,12 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   float alpha, beta;
   int vec_a, vec_b;  // rows of A / rows of B may be read as aligned 16-byte vectors
+  // Affine-quantized B (quantized kernels only): B is the packed (N, K * bits
+  // / 32) uint32 weight, qs / qz the (N, K / group) scales and biases in the
+  // element type, group = 1 << qgroup_shift.
+  const void* qs;
+  const void* qz;
+  int qgroup_shift;
 };
 
 // ---------------------------------------------------------------- element types
@@ -171,7 +177,7 @@ struct Slot {
   uint4* b;
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB>
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, int QB = 0>
 struct GemmTile {
   static constexpr int NT = 64 * NW;
   static constexpr int CW = WM * WN;                  // compute waves
@@ -473,6 +479,148 @@ struct GemmTile {
       dma_rounds<false>(slots, nst, nsteps, acc);
   }
 
+  // ---- Affine-quantized B (QB bits per weight; 16-bit elements only).
+  // Weight element k of row n is bits QB * (k % (32 / QB)) of uint32 word
+  // k / (32 / QB) of that row (little-endian packing); it dequantizes to
+  // T(fp32(scale * q + bias)) with the scale and bias of group k / group.
+  // scale * q is exact in fp32 (at most 11 + 8 significant bits), so this is
+  // one rounding to fp32 and one to T -- the same value as dequantizing the
+  // whole matrix to T first. The dequantized B tile is written to LDS in the
+  // dense layout, and the MFMA loop is the dense one: the result is the
+  // dense GEMM on the dequantized weight, bit for bit.
+  static constexpr int QP = NW == 8 ? 2 : 4;  // stages of loads in flight (registers)
+  static_assert(QB == 0 || (TB && sizeof(T) == 2 && (QB == 2 || QB == 4 || QB == 8)),
+                "quantized B: (N, K) layout, 16-bit elements, 2/4/8 bits");
+  struct QStage {
+    uint4 a[LA];
+    uint2 w[LB];     // packed bits of the 8 weights of B chunk i
+    uint32_t sz[LB];  // scale (low half) and bias (high half) of that chunk, element bits
+  };
+  __amdgpu_buffer_rsrc_t rs_src, rz_src;
+  int64_t qrow_bytes;
+  int qgshift;
+
+  __device__ __forceinline__ void init_buffers_q(const GemmArgs& p) {
+    constexpr int64_t E = sizeof(T);
+    ra_src = make_rsrc(A + m0 * K, min((int64_t)BM, M - m0) * K * E);
+    qrow_bytes = K * QB / 8;
+    const int64_t rows = min((int64_t)BN, N - n0);
+    rb_src = make_rsrc(reinterpret_cast<const char*>(B) + n0 * qrow_bytes, rows * qrow_bytes);
+    qgshift = p.qgroup_shift;
+    const int64_t G = K >> qgshift;  // groups per row
+    rs_src = make_rsrc(static_cast<const T*>(p.qs) + n0 * G, rows * G * E);
+    rz_src = make_rsrc(static_cast<const T*>(p.qz) + n0 * G, rows * G * E);
+  }
+
+  __device__ __forceinline__ void qload(int64_t s, QStage& st) const {
+    constexpr uint32_t E = sizeof(T);
+    const int64_t k0 = s * EPS;
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+      const int q = tid + i * NT;
+      if (A_CH % NT == 0 || q < A_CH) {
+        const int r = q / RC, c = q % RC;
+        const int64_t k = k0 + c * EPC;
+        st.a[i] = buffer_chunk(ra_src, k < K ? (uint32_t)((r * K + k) * E) : kOutOfRange);
+      }
+    }
+    const int64_t G = K >> qgshift;
+#pragma unroll
+    for (int i = 0; i < LB; i++) {
+      const int q = tid + i * NT;
+      if (B_CH % NT == 0 || q < B_CH) {
+        const int r = q / RC, c = q % RC;
+        const int64_t k = k0 + c * EPC;  // first of the chunk's 8 weights
+        const bool in = k < K;
+        const uint32_t wo = in ? (uint32_t)(r * qrow_bytes + k * QB / 8) : kOutOfRange;
+        if constexpr (QB == 8) {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b64(rb_src, (int)wo, 0, 0);
+          st.w[i] = __builtin_bit_cast(uint2, v);
+        } else if constexpr (QB == 4) {
+          st.w[i] = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(rb_src, (int)wo, 0, 0), 0u);
+        } else {
+          st.w[i] = make_uint2(__builtin_amdgcn_raw_buffer_load_b16(rb_src, (int)wo, 0, 0), 0u);
+        }
+        const uint32_t go = in ? (uint32_t)((r * G + (k >> qgshift)) * E) : kOutOfRange;
+        const uint32_t sc = __builtin_amdgcn_raw_buffer_load_b16(rs_src, (int)go, 0, 0);
+        const uint32_t zb = __builtin_amdgcn_raw_buffer_load_b16(rz_src, (int)go, 0, 0);
+        st.sz[i] = sc | (zb << 16);
+      }
+    }
+  }
+
+  __device__ __forceinline__ static float bits_to_f32(uint32_t b16) {
+    return Elem<T>::to_f32(__builtin_bit_cast(T, (unsigned short)b16));
+  }
+
+  __device__ __forceinline__ void qstore(Slot sl, const QStage& st) const {
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+      const int q = tid + i * NT;
+      if (A_CH % NT == 0 || q < A_CH) {
+        const int r = q / RC, c = q % RC;
+        sl.a[r * RC + (c ^ swz_k(r))] = st.a[i];
+      }
+    }
+    constexpr uint32_t MASK = (1u << QB) - 1u;
+#pragma unroll
+    for (int i = 0; i < LB; i++) {
+      const int q = tid + i * NT;
+      if (B_CH % NT == 0 || q < B_CH) {
+        const int r = q / RC, c = q % RC;
+        const float sc = bits_to_f32(st.sz[i] & 0xFFFFu);
+        const float zb = bits_to_f32(st.sz[i] >> 16);
+        unsigned short e[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const uint32_t word = (QB == 8 && t >= 4) ? st.w[i].y : st.w[i].x;
+          const int sh = QB == 8 ? 8 * (t & 3) : QB * t;
+          const float qv = (float)((word >> sh) & MASK);
+          e[t] = __builtin_bit_cast(unsigned short, Elem<T>::from_f32(__builtin_fmaf(sc, qv, zb)));
+        }
+        uint4 v;
+        v.x = e[0] | ((uint32_t)e[1] << 16);
+        v.y = e[2] | ((uint32_t)e[3] << 16);
+        v.z = e[4] | ((uint32_t)e[5] << 16);
+        v.w = e[6] | ((uint32_t)e[7] << 16);
+        sl.b[r * RC + (c ^ swz_k(r))] = v;
+      }
+    }
+  }
+
+  // Loads run QP stages ahead in registers; each stage is dequantized into
+  // one of two LDS slots one stage before it is computed (whole rounds of QP
+  // stages, so ring indices are compile-time).
+  template <bool COMPUTE, typename Slots>
+  __device__ __forceinline__ void q_rounds(const Slots& slots, int64_t nst, int64_t nsteps,
+                                           QStage (&q)[QP], f32x4_t (&acc)[CHAINS][FM][FN]) const {
+    for (int64_t s0 = 0; s0 < nst; s0 += QP) {
+#pragma unroll
+      for (int u = 0; u < QP; u++) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+        asm volatile("s_barrier" ::: "memory");
+        qstore(slots((u + 1) & 1), q[(u + 1) % QP]);
+        qload(s0 + u + 1 + QP, q[(u + 1) % QP]);
+        if constexpr (COMPUTE) compute(slots(u & 1), steps_of(nsteps, s0 + u), acc);
+      }
+    }
+  }
+
+  template <typename Slots>
+  __device__ __forceinline__ void main_loop_q(const Slots& slots, int64_t nst, int64_t nsteps,
+                                              bool computes, f32x4_t (&acc)[CHAINS][FM][FN]) const {
+    static_assert(QP % 2 == 0, "ring of two LDS slots");
+    QStage q[QP];
+#pragma unroll
+    for (int u = 0; u < QP; u++) qload(u, q[u]);
+    qstore(slots(0), q[0]);
+    qload(QP, q[0]);
+    if (computes)
+      q_rounds<true>(slots, nst, nsteps, q, acc);
+    else
+      q_rounds<false>(slots, nst, nsteps, q, acc);
+  }
+
   // Register-staged path (unaligned operands): two slots, double buffered.
   template <typename Slots>
   __device__ __forceinline__ void main_loop_slow(const Slots& slots, int64_t nst,
@@ -490,9 +638,9 @@ struct GemmTile {
   }
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB>
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, int QB = 0>
 __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
-  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB>;
+  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB, QB>;
   constexpr int FM = Tile::FM, FN = Tile::FN, CHAINS = Tile::CHAINS;
   constexpr int AC = Tile::A_CH, BC = Tile::B_CH;
   // The LDS ring: NS stages, each an A and a B array (unused ones are a single chunk).
@@ -549,7 +697,11 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
       for (int jn = 0; jn < FN; jn++) acc[ch][i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   t.init_lds_offsets();
-  if (p.vec_a && p.vec_b) {
+  if constexpr (QB > 0) {
+    // The host launches quantized kernels only with 16-byte aligned rows of A.
+    t.init_buffers_q(p);
+    t.main_loop_q(slots, nst, nsteps, computes, acc);
+  } else if (p.vec_a && p.vec_b) {
     t.init_buffers();
     t.init_dma();
     t.main_loop_dma(slots, nst, nsteps, computes, acc);
@@ -609,9 +761,27 @@ KernelFn kernel_for(int g, bool trans_b) {
   return nullptr;
 }
 
+// Quantized-B kernel for geometry g (16-bit element types; (N, K) packed B).
+template <typename T>
+KernelFn qkernel_for(int g, int bits) {
+#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns)                          \
+  case id:                                                                    \
+    switch (bits) {                                                           \
+      case 2: return gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, 2>;     \
+      case 4: return gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, 4>;     \
+      case 8: return gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, 8>;     \
+    }                                                                         \
+    return nullptr;
+  switch (g) { BI_GEOMETRIES(BI_QGEO_CASE) }
+#undef BI_QGEO_CASE
+  return nullptr;
+}
+
 }  // namespace bi_gemm_dev
 
 // Per-type kernel tables, defined in bi_gemm_{f32,f16,bf16}.hip.
 bi_gemm_dev::KernelFn bi_gemm_kernel_f32(int g, bool trans_b);
 bi_gemm_dev::KernelFn bi_gemm_kernel_f16(int g, bool trans_b);
 bi_gemm_dev::KernelFn bi_gemm_kernel_bf16(int g, bool trans_b);
+bi_gemm_dev::KernelFn bi_qgemm_kernel_f16(int g, int bits);
+bi_gemm_dev::KernelFn bi_qgemm_kernel_bf16(int g, int bits);

@@ -20,7 +20,7 @@ BUILD = os.path.join(PKG_ROOT, "_build")
 LIB = os.path.join(PKG_ROOT, "mlx_batch_invariant", "libbi.so")
 
 SOURCES = ["bi_abi.cpp", "bi_gemm.hip", "bi_gemm_f32.hip", "bi_gemm_f16.hip", "bi_gemm_bf16.hip",
-           "bi_sdpa.hip"]
+           "bi_qgemm_f16.hip", "bi_qgemm_bf16.hip", "bi_sdpa.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

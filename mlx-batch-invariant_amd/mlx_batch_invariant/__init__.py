@@ -25,12 +25,20 @@ import torch.nn.functional as F
 from ._attention import HEAD_DIMS, scaled_dot_product_attention, supported_head_dims
 from ._attention import _mask_args, _sdpa
 from ._gemm import TILE, addmm, geometries, linear, matmul
+from ._quant import (QUANT_BITS, QuantizedLinear, dequantize, quantize, quantized_linear,
+                     quantized_matmul)
 
 __all__ = [
     "matmul",
     "addmm",
     "linear",
     "scaled_dot_product_attention",
+    "quantized_linear",
+    "quantized_matmul",
+    "quantize",
+    "dequantize",
+    "QuantizedLinear",
+    "QUANT_BITS",
     "batch_invariant_mode",
     "is_enabled",
     "TILE",
@@ -41,12 +49,18 @@ __all__ = [
 __version__ = "0.2.0"
 
 _depth = 0
+_strict_flag = True
 _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
 
 
 def is_enabled():
     """True inside a :func:`batch_invariant_mode` block (reference __init__.py:41-43)."""
     return _depth > 0
+
+
+def _strict():
+    """strict= of the outermost active batch_invariant_mode."""
+    return _strict_flag
 
 
 def _unsupported(what, strict, fallback, *args, **kwargs):
@@ -109,7 +123,7 @@ def batch_invariant_mode(strict=True):
     Process-global and not thread-safe, like the reference: it patches module
     attributes. Nesting is counted; only the outermost exit restores.
     """
-    global _depth
+    global _depth, _strict_flag
 
     if _depth:  # already patched; nesting must not stack another set of shims
         _depth += 1
@@ -203,10 +217,12 @@ def batch_invariant_mode(strict=True):
     patches.set(F, "linear", bi_linear)
     patches.set(F, "scaled_dot_product_attention", bi_sdpa)
     _depth = 1
+    _strict_flag = bool(strict)
     try:
         yield
     finally:
         _depth = 0
+        _strict_flag = True
         patches.restore()
 
 

@@ -1,11 +1,12 @@
-"""torch.library custom ops over the two kernel launches, for torch.compile.
+"""torch.library custom ops over the kernel launches, for torch.compile.
 
 The reference's kernels are opaque to ``mx.compile``, which may reorder and
 fuse the graph around them but never inside (reference
 tests/test_invariance.py:595-640). The same holds here: while torch.compile
-traces, ``bi.*`` calls become the ops ``mlx_bi::gemm`` and ``mlx_bi::sdpa``,
-which the compiler treats as opaque nodes (their fake implementations give
-only output shapes) and which run the HIP kernels unchanged. Eager calls skip
+traces, ``bi.*`` calls become the ops ``mlx_bi::gemm``, ``mlx_bi::qgemm`` and
+``mlx_bi::sdpa``, which the compiler treats as opaque nodes (their fake
+implementations give only output shapes) and which run the HIP kernels
+unchanged. Eager calls skip
 the dispatcher and launch directly.
 """
 
@@ -41,3 +42,16 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, mask_m
 @sdpa.register_fake
 def _sdpa_fake(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks):
     return q.new_empty((q.shape[0], q.shape[1], q.shape[2], v.shape[-1]))
+
+
+@torch.library.custom_op("mlx_bi::qgemm", mutates_args=())
+def qgemm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+          group_size: int, bits: int) -> torch.Tensor:
+    from . import _quant
+
+    return _quant._quantized_linear_eager(x, w, scales, biases, group_size, bits)
+
+
+@qgemm.register_fake
+def _qgemm_fake(x, w, scales, biases, group_size, bits):
+    return x.new_empty((*x.shape[:-1], w.shape[0]))

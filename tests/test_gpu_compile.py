@@ -1,7 +1,7 @@
 """torch.compile around the invariant kernels (reference
 tests/test_invariance.py:595-640, TestCompiled). The compiler may reorder and
 fuse the graph around them, never inside: traced calls become the opaque ops
-mlx_bi::gemm / mlx_bi::sdpa, with no graph break. backend="aot_eager" traces
+mlx_bi::gemm / mlx_bi::qgemm / mlx_bi::sdpa, with no graph break. backend="aot_eager" traces
 through Dynamo and AOTAutograd and runs the graph's kernels as they are, so
 no code is generated for the surrounding ops."""
 
@@ -80,3 +80,12 @@ def test_ops_pass_opcheck(cuda):
     q = rn((1, 4, 3, 64), torch.bfloat16, 62, device=cuda)
     k = rn((1, 2, 40, 64), torch.bfloat16, 63, device=cuda)
     torch.library.opcheck(_ops.sdpa, (q, k, k, 0.125, 1, None, [0, 0, 0], 37, None))
+    wq, s, b = bi.quantize(rn((64, 256), torch.bfloat16, 64), 64, 4)
+    torch.library.opcheck(_ops.qgemm, (a, wq.to(cuda), s.to(cuda), b.to(cuda), 64, 4))
+
+
+def test_compiled_quantized_linear_matches_eager(cuda):
+    wq, s, b = (t.to(cuda) for t in bi.quantize(rn((256, 512), torch.float16, 65), 32, 8))
+    x = rn((3, 5, 512), torch.float16, 66, device=cuda)
+    fn = _compile(lambda t: bi.quantized_linear(t, wq, s, b, 32, 8) * 2, fullgraph=True)
+    assert np.array_equal(bits(fn(x)), bits(bi.quantized_linear(x, wq, s, b, 32, 8) * 2))

@@ -342,3 +342,57 @@ def test_custom_op_fake_shapes():
         q, k = torch.empty(2, 8, 3, 64), torch.empty(2, 2, 10, 64)
         assert _ops.sdpa(q, k, torch.empty(2, 2, 10, 32), 0.1, 0, None, [0, 0, 0], 0,
                          None).shape == (2, 8, 3, 32)
+
+
+def test_quant_pack_layout_matches_the_oracle():
+    """bi's packing is the reference layout: the oracle's restatement of the
+    reference unpack reads back the codes bi packed; dequantize agrees bitwise."""
+    from oracle import quant as oquant
+
+    from mlx_batch_invariant import _quant
+
+    g = torch.Generator().manual_seed(7)
+    for bits in bi.QUANT_BITS:
+        q = torch.randint(0, 1 << bits, (6, 128), generator=g)
+        w = _quant._pack(q, bits)
+        assert w.dtype == torch.int32 and w.shape == (6, 128 * bits // 32)
+        assert torch.equal(_quant._unpack(w, bits, 128), q)
+        assert (oquant.unpack(w.numpy(), bits, 128) == q.numpy()).all()
+        for dtype, name in ((torch.bfloat16, "bfloat16"), (torch.float16, "float16")):
+            for gs in (32, 64, 128):
+                s = (torch.rand(6, 128 // gs, generator=g) * 0.1 + 1e-3).to(dtype)
+                b = (torch.randn(6, 128 // gs, generator=g)).to(dtype)
+                got = bi.dequantize(w, s, b, gs, bits)
+                want = oquant.dequantize(w.numpy(), s.float().numpy(), b.float().numpy(), gs,
+                                         bits, name)
+                assert got.dtype == dtype
+                assert (got.double().numpy() == want).all(), (bits, name, gs)
+
+
+def test_quantize_error_is_within_half_a_step():
+    g = torch.Generator().manual_seed(8)
+    w = torch.randn(32, 256, generator=g).to(torch.bfloat16)
+    for bits in bi.QUANT_BITS:
+        for gs in (32, 64, 128):
+            q, s, b = bi.quantize(w, gs, bits)
+            err = (bi.dequantize(q, s, b, gs, bits).float() - w.float()).abs()
+            step = s.float().repeat_interleave(gs, dim=1)
+            assert (err <= step * 0.5 + w.float().abs() * 2 ** -7 + 1e-6).all(), (bits, gs)
+
+
+def test_quantized_linear_validation():
+    x = torch.zeros(3, 128, dtype=torch.bfloat16)
+    w, s, b = bi.quantize(torch.zeros(64, 128, dtype=torch.bfloat16), 64, 4)
+    with pytest.raises(ValueError):
+        bi.quantized_linear(x, w, s, b, 64, 3)            # bits
+    with pytest.raises(ValueError):
+        bi.quantized_linear(x[:, :96], w, s, b, 64, 4)    # K mismatch
+    with pytest.raises(ValueError):
+        bi.quantized_linear(x, w, s[:, :1], b, 64, 4)     # scales shape
+    with pytest.raises(ValueError):
+        bi.quantized_linear(x, w, s.float(), b, 64, 4)    # scales dtype
+    with pytest.raises(ValueError):
+        bi.quantized_linear(x, w, s, b, 64, 4)            # CPU tensors
+    # outside the mode quantized_matmul is stock: dequantize, then F.linear
+    y = bi.quantized_matmul(x, w, s, b, True, 64, 4)
+    assert torch.equal(y, F.linear(x, bi.dequantize(w, s, b, 64, 4)))

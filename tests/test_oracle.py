@@ -301,3 +301,49 @@ def test_planted_sdpa_mistakes_are_caught():
 
     for bad in (wrong_gqa, top_left_causal, unscaled):
         assert not _sdpa_checks_pass(bad), bad.__name__
+
+
+# ---------------------------------------------------------------- quantized weights
+
+def _big_endian_unpack(words, bits, K):
+    """A planted mistake: codes taken from the high end of each word."""
+    per = 32 // bits
+    w = np.asarray(words).astype(np.int64) & 0xFFFFFFFF
+    q = np.empty((w.shape[0], K), dtype=np.int64)
+    for k in range(K):
+        q[:, k] = (w[:, k // per] >> (bits * (per - 1 - k % per))) & ((1 << bits) - 1)
+    return q
+
+
+QUANT_KATS = [
+    # (bits, words of one row, codes of that row): worked by hand
+    (4, [0x76543210, 0xFEDCBA98], list(range(16))),
+    (8, [0x04030201, 0x000000FF], [1, 2, 3, 4, 255, 0, 0, 0]),
+    (2, [0x1BE4], [0, 1, 2, 3, 3, 2, 1, 0] + [0] * 8),
+]
+
+
+@pytest.mark.parametrize("i", range(len(QUANT_KATS)))
+def test_quant_unpack_known_words(i):
+    from oracle import quant as oquant
+
+    bits, words, codes = QUANT_KATS[i]
+    got = oquant.unpack(np.array([words], dtype=np.int64), bits, len(codes))
+    assert got.tolist() == [codes]
+    # the planted big-endian reading disagrees with the hand-worked codes
+    assert _big_endian_unpack(np.array([words]), bits, len(codes)).tolist() != [codes]
+
+
+def test_quant_dequantize_closed_form_and_rounding():
+    from oracle import quant as oquant
+
+    # scale 0.5, bias -1: every value -1 + q/2 is exact in every element type
+    words = np.array([[0x76543210, 0xFEDCBA98]], dtype=np.int64)
+    got = oquant.dequantize(words, [[0.5]], [[-1.0]], 16, 4, "bfloat16")
+    assert got.tolist() == [[-1.0 + q / 2 for q in range(16)]]
+    # 1 + 3 * 2**-9 is not a bfloat16: the fp32 value rounds once to the element type
+    words = np.array([[0x3]], dtype=np.int64)
+    s, b = 2.0 ** -9, 1.0
+    got = oquant.dequantize(words, [[s]], [[b]], 16, 2, "bfloat16")[0, 0]
+    want = float(torch.tensor(1 + 3 * s, dtype=torch.float32).to(torch.bfloat16).float())
+    assert got == want and got != 1 + 3 * s
