@@ -124,13 +124,18 @@ int bi_sdpa(const void* q, const void* k, const void* v,
  *           row n is bits bits * (k % (32 / bits)) .. of word k / (32 / bits)
  *           of that row (little-endian packing, the MLX affine layout)
  *   scales, (N, K / group_size) in the element type of x; element k of row n
- *   biases  dequantizes to T(fp32(scales[n][k/group] * q + biases[n][k/group]))
+ *   biases  dequantizes to the fp32 value
+ *           v = fp32(scales[n][k/group] * q + biases[n][k/group])
  *   out     (M, N) row-major
  *   bits in {2, 4, 8}; group_size in {32, 64, 128} and dividing K.
  *
- * The result is bitwise that of bi_gemm (trans_b = 1, no bias) on the
- * dequantized weight, with the same invariance: nothing depends on M or on a
- * row's batch neighbours. BI_F32 activations return BI_EUNSUPPORTED.
+ * As in the reference kernel (a float B tile, _gemm.py:46, :170-173), v is
+ * not rounded to the element type: each product x * v reaches the fp32
+ * accumulator exactly for bf16 (v as three bf16 planes) and to 2^-22 |v| for
+ * f16 (two f16 planes, the second scaled by 2^11 into its own chain), in a
+ * fixed order per 32-element chunk of K; the output is rounded once. Nothing
+ * depends on M or on a row's batch neighbours. BI_F32 activations return
+ * BI_EUNSUPPORTED.
  */
 int bi_qgemm(const void* x, const void* w, const void* scales, const void* biases, void* out,
              int64_t M, int64_t N, int64_t K, int group_size, int bits, int dtype,

@@ -72,6 +72,9 @@ template <> struct Elem<_Float16> {
   __device__ static float to_f32(_Float16 x) { return (float)x; }
   __device__ static _Float16 from_f32(float x) { return (_Float16)x; }  // RNE
 };
+template <typename T> struct IsBF16 { static constexpr bool value = false; };
+template <> struct IsBF16<__bf16> { static constexpr bool value = true; };
+
 template <> struct Elem<float> {
   __device__ static float to_f32(float x) { return x; }
   __device__ static float from_f32(float x) { return x; }
@@ -175,6 +178,12 @@ constexpr int waitcnt_vm_lgkm0(int vm) {
 struct Slot {
   uint4* a;
   uint4* b;
+};
+// One stage of the quantized kernel's two-slot ring: the A tile and the B
+// tile's 16-bit planes (the third is unused for f16).
+struct QSlot {
+  uint4* a;
+  uint4* b[3];
 };
 
 template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, int QB = 0>
@@ -481,14 +490,23 @@ struct GemmTile {
 
   // ---- Affine-quantized B (QB bits per weight; 16-bit elements only).
   // Weight element k of row n is bits QB * (k % (32 / QB)) of uint32 word
-  // k / (32 / QB) of that row (little-endian packing); it dequantizes to
-  // T(fp32(scale * q + bias)) with the scale and bias of group k / group.
-  // scale * q is exact in fp32 (at most 11 + 8 significant bits), so this is
-  // one rounding to fp32 and one to T -- the same value as dequantizing the
-  // whole matrix to T first. The dequantized B tile is written to LDS in the
-  // dense layout, and the MFMA loop is the dense one: the result is the
-  // dense GEMM on the dequantized weight, bit for bit.
+  // k / (32 / QB) of that row (little-endian packing). It dequantizes to the
+  // fp32 value v = fp32(scale * q + bias) with the scale and bias of group
+  // k / group (scale * q is exact in fp32, so v has one rounding), and v enters
+  // the product in fp32. The MFMAs take 16-bit operands, so v is written to LDS
+  // as 16-bit planes whose products with the activation are exact in fp32:
+  //   bf16: v = h1 + h2 + h3, each the top 8 significant bits of what is left
+  //         (truncation, so every subtraction is exact and h3 is a bf16);
+  //         x * h1, x * h2, x * h3 accumulate into one fp32 chain, in that
+  //         order, in each chunk-step.
+  //   f16:  h1 = f16(v) (RNE), h2 = f16((v - h1) * 2^11); x * h1 and x * h2
+  //         accumulate into two chains that the epilogue joins as
+  //         fma(2^-11, chain_2, chain_1). h1 + 2^-11 h2 equals v to within
+  //         2^-22 |v| (2^-36 absolute for |v| < 2^-14, below f16's normal range).
   static constexpr int QP = NW == 8 ? 2 : 4;  // stages of loads in flight (registers)
+  static constexpr bool QBF16 = IsBF16<T>::value;
+  static constexpr int QPL = QBF16 ? 3 : 2;   // 16-bit planes per weight
+  static constexpr int QACC = QBF16 ? 1 : 2;  // fp32 chains per output element
   static_assert(QB == 0 || (TB && sizeof(T) == 2 && (QB == 2 || QB == 4 || QB == 8)),
                 "quantized B: (N, K) layout, 16-bit elements, 2/4/8 bits");
   struct QStage {
@@ -553,7 +571,29 @@ struct GemmTile {
     return Elem<T>::to_f32(__builtin_bit_cast(T, (unsigned short)b16));
   }
 
-  __device__ __forceinline__ void qstore(Slot sl, const QStage& st) const {
+  // The 16-bit planes of one fp32 weight (low halves of e[0..QPL-1]).
+  __device__ __forceinline__ static void split_planes(float v, uint32_t (&e)[3]) {
+    if constexpr (QBF16) {
+      const uint32_t h1 = __float_as_uint(v) & 0xFFFF0000u;
+      const float r = v - __uint_as_float(h1);
+      const uint32_t h2 = __float_as_uint(r) & 0xFFFF0000u;
+      const uint32_t h3 = __float_as_uint(r - __uint_as_float(h2));
+      e[0] = h1 >> 16;
+      e[1] = h2 >> 16;
+      e[2] = h3 >> 16;
+    } else {
+      const _Float16 h1 = (_Float16)v;
+      const float r = v - (float)h1;
+      const _Float16 h2 = (_Float16)(r * 2048.0f);
+      e[0] = __builtin_bit_cast(unsigned short, h1);
+      e[1] = __builtin_bit_cast(unsigned short, h2);
+      e[2] = 0;
+    }
+  }
+
+  // Stage st into LDS: A as loaded, B dequantized into its QPL planes (each in
+  // the dense (N, K) tile layout).
+  __device__ __forceinline__ void qstore(QSlot sl, const QStage& st) const {
 #pragma unroll
     for (int i = 0; i < LA; i++) {
       const int q = tid + i * NT;
@@ -570,30 +610,68 @@ struct GemmTile {
         const int r = q / RC, c = q % RC;
         const float sc = bits_to_f32(st.sz[i] & 0xFFFFu);
         const float zb = bits_to_f32(st.sz[i] >> 16);
-        unsigned short e[8];
+        uint32_t e[8][3];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
           const uint32_t word = (QB == 8 && t >= 4) ? st.w[i].y : st.w[i].x;
           const int sh = QB == 8 ? 8 * (t & 3) : QB * t;
           const float qv = (float)((word >> sh) & MASK);
-          e[t] = __builtin_bit_cast(unsigned short, Elem<T>::from_f32(__builtin_fmaf(sc, qv, zb)));
+          split_planes(__builtin_fmaf(sc, qv, zb), e[t]);
         }
-        uint4 v;
-        v.x = e[0] | ((uint32_t)e[1] << 16);
-        v.y = e[2] | ((uint32_t)e[3] << 16);
-        v.z = e[4] | ((uint32_t)e[5] << 16);
-        v.w = e[6] | ((uint32_t)e[7] << 16);
-        sl.b[r * RC + (c ^ swz_k(r))] = v;
+        const int at = r * RC + (c ^ swz_k(r));
+#pragma unroll
+        for (int pl = 0; pl < QPL; pl++) {
+          uint4 v;
+          v.x = e[0][pl] | (e[1][pl] << 16);
+          v.y = e[2][pl] | (e[3][pl] << 16);
+          v.z = e[4][pl] | (e[5][pl] << 16);
+          v.w = e[6][pl] | (e[7][pl] << 16);
+          sl.b[pl][at] = v;
+        }
       }
+    }
+  }
+
+  // Chunk-step j of the stage in `sl` for every block of this wave.
+  __device__ __forceinline__ void q_step(QSlot sl, int j, f32x4_t (&acc)[QACC][FM][FN]) const {
+    uint4 av[FM];
+#pragma unroll
+    for (int i = 0; i < FM; i++) av[i] = sl.a[a_off[j] + i * 16 * RC];
+#pragma unroll
+    for (int pl = 0; pl < QPL; pl++) {
+      uint4 bv[FN];
+#pragma unroll
+      for (int jn = 0; jn < FN; jn++) bv[jn] = sl.b[pl][b_off[j] + jn * 16 * RC];
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int jn = 0; jn < FN; jn++) {
+          f32x4_t& c = acc[QBF16 ? 0 : pl][i][jn];
+          c = chunk_step(T(0), av[i], bv[jn], c);
+        }
+    }
+  }
+
+  __device__ __forceinline__ void q_compute(QSlot sl, int steps,
+                                            f32x4_t (&acc)[QACC][FM][FN]) const {
+    if (steps == CS) {
+#pragma unroll
+      for (int j = 0; j < CS; j++) q_step(sl, j, acc);
+    } else {
+#pragma unroll
+      for (int j = 0; j < CS - 1; j++)
+        if (j < steps) q_step(sl, j, acc);
     }
   }
 
   // Loads run QP stages ahead in registers; each stage is dequantized into
   // one of two LDS slots one stage before it is computed (whole rounds of QP
-  // stages, so ring indices are compile-time).
-  template <bool COMPUTE, typename Slots>
-  __device__ __forceinline__ void q_rounds(const Slots& slots, int64_t nst, int64_t nsteps,
-                                           QStage (&q)[QP], f32x4_t (&acc)[CHAINS][FM][FN]) const {
+  // stages, so ring indices are compile-time). Before a slot is rewritten,
+  // the barrier guarantees every wave finished reading it (LDS reads retire
+  // before the barrier: lgkmcnt(0)).
+  template <bool COMPUTE, typename QSlots>
+  __device__ __forceinline__ void q_rounds(const QSlots& slots, int64_t nst, int64_t nsteps,
+                                           QStage (&q)[QP], f32x4_t (&acc)[QACC][FM][FN]) const {
     for (int64_t s0 = 0; s0 < nst; s0 += QP) {
 #pragma unroll
       for (int u = 0; u < QP; u++) {
@@ -601,14 +679,14 @@ struct GemmTile {
         asm volatile("s_barrier" ::: "memory");
         qstore(slots((u + 1) & 1), q[(u + 1) % QP]);
         qload(s0 + u + 1 + QP, q[(u + 1) % QP]);
-        if constexpr (COMPUTE) compute(slots(u & 1), steps_of(nsteps, s0 + u), acc);
+        if constexpr (COMPUTE) q_compute(slots(u & 1), steps_of(nsteps, s0 + u), acc);
       }
     }
   }
 
-  template <typename Slots>
-  __device__ __forceinline__ void main_loop_q(const Slots& slots, int64_t nst, int64_t nsteps,
-                                              bool computes, f32x4_t (&acc)[CHAINS][FM][FN]) const {
+  template <typename QSlots>
+  __device__ __forceinline__ void main_loop_q(const QSlots& slots, int64_t nst, int64_t nsteps,
+                                              bool computes, f32x4_t (&acc)[QACC][FM][FN]) const {
     static_assert(QP % 2 == 0, "ring of two LDS slots");
     QStage q[QP];
 #pragma unroll
@@ -638,9 +716,9 @@ struct GemmTile {
   }
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, int QB = 0>
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB>
 __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
-  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB, QB>;
+  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB>;
   constexpr int FM = Tile::FM, FN = Tile::FN, CHAINS = Tile::CHAINS;
   constexpr int AC = Tile::A_CH, BC = Tile::B_CH;
   // The LDS ring: NS stages, each an A and a B array (unused ones are a single chunk).
@@ -697,11 +775,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
       for (int jn = 0; jn < FN; jn++) acc[ch][i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   t.init_lds_offsets();
-  if constexpr (QB > 0) {
-    // The host launches quantized kernels only with 16-byte aligned rows of A.
-    t.init_buffers_q(p);
-    t.main_loop_q(slots, nst, nsteps, computes, acc);
-  } else if (p.vec_a && p.vec_b) {
+  if (p.vec_a && p.vec_b) {
     t.init_buffers();
     t.init_dma();
     t.main_loop_dma(slots, nst, nsteps, computes, acc);
@@ -728,6 +802,81 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
           float v = acc[0][i][jn][e];
           if constexpr (CHAINS == 2) v = v + acc[1][i][jn][e];
           if (bias) v = __builtin_fmaf(alpha, v, bv);
+          out[row * N + col] = Elem<T>::from_f32(v);
+        }
+      }
+    }
+  }
+}
+
+// Quantized-B GEMM: the dense kernel's tile walk and chunk-step order, with B
+// dequantized to fp32 and held as 16-bit planes (GemmTile's quantized part).
+// Every output element sees, per chunk-step, the planes' MFMAs in a fixed
+// order on its own row of A and column of B; the footprint only decides which
+// elements a workgroup owns. Epilogue: bf16 acc, f16 fma(2^-11, chain_2,
+// chain_1); then one RNE rounding.
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int QB>
+__global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
+  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, 2, true, QB>;
+  constexpr int FM = Tile::FM, FN = Tile::FN, QACC = Tile::QACC, QPL = Tile::QPL;
+  constexpr int AC = Tile::A_CH, BC = Tile::B_CH, BC3 = QPL > 2 ? BC : 1;
+  __shared__ uint4 a0[AC], p00[BC], p01[BC], p02[BC3];
+  __shared__ uint4 a1[AC], p10[BC], p11[BC], p12[BC3];
+  auto slots = [&](int u) -> QSlot {
+    if (u == 0) return {a0, {p00, p01, p02}};
+    return {a1, {p10, p11, p12}};
+  };
+
+  Tile t;
+  t.A = static_cast<const T*>(p.a);
+  t.B = static_cast<const T*>(p.b);
+  t.M = p.M;
+  t.N = p.N;
+  t.K = p.K;
+  t.tid = threadIdx.x;
+  t.lane = t.tid & 63;
+  t.wave = __builtin_amdgcn_readfirstlane(t.tid >> 6);
+  t.wm = (t.wave % Tile::CW) / WN;
+  t.wn = (t.wave % Tile::CW) % WN;
+  t.g = t.lane >> 4;
+  t.r16 = t.lane & 15;
+  const int tile = xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n);
+  t.m0 = (int64_t)(tile % p.tiles_m) * BM;
+  t.n0 = (int64_t)(tile / p.tiles_m) * BN;
+
+  const int64_t M = t.M, N = t.N, K = t.K;
+  const int64_t nst = (K + Tile::EPS - 1) / Tile::EPS;
+  const int64_t nsteps = (K + 4 * Tile::EPC - 1) / (4 * Tile::EPC);
+  const int64_t wrow = t.m0 + t.wm * Tile::WTM, wcol = t.n0 + t.wn * Tile::WTN;
+  const bool computes = t.wave < Tile::CW && wrow < M && wcol < N;
+
+  f32x4_t acc[QACC][FM][FN];
+#pragma unroll
+  for (int ch = 0; ch < QACC; ch++)
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int jn = 0; jn < FN; jn++) acc[ch][i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  t.init_lds_offsets();
+  // The host launches quantized kernels only with 16-byte aligned rows of A.
+  t.init_buffers_q(p);
+  t.main_loop_q(slots, nst, nsteps, computes, acc);
+
+  if (!computes) return;
+  T* __restrict__ out = static_cast<T*>(p.out);
+#pragma unroll
+  for (int jn = 0; jn < FN; jn++) {
+    const int64_t col = wcol + jn * 16 + t.r16;
+    if (col >= N) continue;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int64_t row = wrow + i * 16 + 4 * t.g + e;
+        if (row < M) {
+          float v = acc[0][i][jn][e];
+          if constexpr (QACC == 2) v = __builtin_fmaf(0x1p-11f, acc[QACC - 1][i][jn][e], v);
           out[row * N + col] = Elem<T>::from_f32(v);
         }
       }
@@ -762,15 +911,19 @@ KernelFn kernel_for(int g, bool trans_b) {
 }
 
 // Quantized-B kernel for geometry g (16-bit element types; (N, K) packed B).
+// Two LDS slots of A plus the B planes; the 256 x 128 footprint would need
+// 160 KB of LDS and is not built.
 template <typename T>
 KernelFn qkernel_for(int g, int bits) {
-#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns)                          \
-  case id:                                                                    \
-    switch (bits) {                                                           \
-      case 2: return gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, 2>;     \
-      case 4: return gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, 4>;     \
-      case 8: return gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, 8>;     \
-    }                                                                         \
+#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns)                       \
+  case id:                                                                 \
+    if constexpr (bm * bn <= 128 * 128) {                                  \
+      switch (bits) {                                                      \
+        case 2: return gemm_qkernel<T, bm, bn, wm, wn, nw, kb, 2>;         \
+        case 4: return gemm_qkernel<T, bm, bn, wm, wn, nw, kb, 4>;         \
+        case 8: return gemm_qkernel<T, bm, bn, wm, wn, nw, kb, 8>;         \
+      }                                                                    \
+    }                                                                      \
     return nullptr;
   switch (g) { BI_GEOMETRIES(BI_QGEO_CASE) }
 #undef BI_QGEO_CASE

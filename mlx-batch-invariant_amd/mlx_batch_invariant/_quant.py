@@ -9,14 +9,19 @@ dequantized weight) and the shim's ``quantized_matmul`` route
 Weight format (MLX's affine layout): ``w`` is (N, K * bits / 32) 32-bit words;
 weight element k of row n sits in bits ``bits * (k % (32 / bits))`` onward of
 word ``k // (32 / bits)`` of row n (little-endian packing). ``scales`` and
-``biases`` are (N, K / group_size) in the activation dtype, and the element
-dequantizes to ``T(fp32(scale * q + bias))``. Torch has no uint32 arithmetic,
-so packed words are held in int32 tensors (same bits); uint32 is accepted too.
+``biases`` are (N, K / group_size) in the activation dtype. Torch has no
+uint32 arithmetic, so packed words are held in int32 tensors (same bits);
+uint32 is accepted too.
 
-The kernel's result is, bit for bit, ``bi.linear(x, dequantize(w, ...))``:
-it dequantizes each weight exactly as :func:`dequantize` does (``scale * q``
-is exact in fp32, so fusing the add changes nothing) and then runs the dense
-invariant GEMM's arithmetic. Invariance carries over unchanged.
+Arithmetic, as the reference's kernel (_gemm.py:170-173 into a float B tile):
+each weight dequantizes to the fp32 value ``v = fp32(scale * q + bias)`` and
+enters the product unrounded; accumulation is fp32 and the output is rounded
+once. The kernel feeds v to 16-bit MFMAs as planes whose products are exact
+(bf16: three planes, exact; f16: two, to 2^-22 |v|), in a fixed order per
+chunk of K, so invariance holds exactly as for the dense GEMM. Note that
+:func:`dequantize` returns v rounded to the element type (what
+``mx.dequantize`` returns); ``linear(x, dequantize(w))`` therefore differs from
+``quantized_linear`` by that rounding of the weights.
 """
 
 import torch
@@ -73,7 +78,8 @@ def quantize(w, group_size=64, bits=4):
 
 
 def dequantize(w, scales, biases, group_size=64, bits=4):
-    """The (N, K) weight in the dtype of ``scales``: T(fp32(scale * q + bias))."""
+    """The (N, K) weight in the dtype of ``scales``: T(fp32(scale * q + bias)),
+    one rounding of the fp32 value the quantized GEMM multiplies by."""
     if bits not in QUANT_BITS:
         raise ValueError("bits must be one of %s, got %r" % (QUANT_BITS, bits))
     K = w.shape[1] * (32 // bits)

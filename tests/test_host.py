@@ -346,9 +346,11 @@ def test_custom_op_fake_shapes():
 
 def test_quant_pack_layout_matches_the_oracle():
     """bi's packing is the reference layout: the oracle's restatement of the
-    reference unpack reads back the codes bi packed; dequantize agrees bitwise."""
+    reference unpack reads back the codes bi packed; bi.dequantize is the
+    oracle's fp32 weight rounded once to the element type."""
     from oracle import quant as oquant
 
+    from helpers import pack_codes
     from mlx_batch_invariant import _quant
 
     g = torch.Generator().manual_seed(7)
@@ -356,6 +358,7 @@ def test_quant_pack_layout_matches_the_oracle():
         q = torch.randint(0, 1 << bits, (6, 128), generator=g)
         w = _quant._pack(q, bits)
         assert w.dtype == torch.int32 and w.shape == (6, 128 * bits // 32)
+        assert torch.equal(w, pack_codes(q.numpy(), bits))
         assert torch.equal(_quant._unpack(w, bits, 128), q)
         assert (oquant.unpack(w.numpy(), bits, 128) == q.numpy()).all()
         for dtype, name in ((torch.bfloat16, "bfloat16"), (torch.float16, "float16")):
@@ -363,8 +366,8 @@ def test_quant_pack_layout_matches_the_oracle():
                 s = (torch.rand(6, 128 // gs, generator=g) * 0.1 + 1e-3).to(dtype)
                 b = (torch.randn(6, 128 // gs, generator=g)).to(dtype)
                 got = bi.dequantize(w, s, b, gs, bits)
-                want = oquant.dequantize(w.numpy(), s.float().numpy(), b.float().numpy(), gs,
-                                         bits, name)
+                want = oquant.dequantize_to(w.numpy(), s.float().numpy(), b.float().numpy(),
+                                            gs, bits, name)
                 assert got.dtype == dtype
                 assert (got.double().numpy() == want).all(), (bits, name, gs)
 

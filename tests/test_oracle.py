@@ -337,13 +337,42 @@ def test_quant_unpack_known_words(i):
 def test_quant_dequantize_closed_form_and_rounding():
     from oracle import quant as oquant
 
-    # scale 0.5, bias -1: every value -1 + q/2 is exact in every element type
+    # scale 0.5, bias -1: every value -1 + q/2 is exact
     words = np.array([[0x76543210, 0xFEDCBA98]], dtype=np.int64)
-    got = oquant.dequantize(words, [[0.5]], [[-1.0]], 16, 4, "bfloat16")
+    got = oquant.dequantize(words, [[0.5]], [[-1.0]], 16, 4)
     assert got.tolist() == [[-1.0 + q / 2 for q in range(16)]]
-    # 1 + 3 * 2**-9 is not a bfloat16: the fp32 value rounds once to the element type
+    # 1 + 3 * 2**-9 is an fp32 value and not a bfloat16: the reference keeps it
+    # in fp32; dequantize_to rounds it once to the element type
     words = np.array([[0x3]], dtype=np.int64)
     s, b = 2.0 ** -9, 1.0
-    got = oquant.dequantize(words, [[s]], [[b]], 16, 2, "bfloat16")[0, 0]
+    assert oquant.dequantize(words, [[s]], [[b]], 16, 2)[0, 0] == 1 + 3 * s
+    got = oquant.dequantize_to(words, [[s]], [[b]], 16, 2, "bfloat16")[0, 0]
     want = float(torch.tensor(1 + 3 * s, dtype=torch.float32).to(torch.bfloat16).float())
     assert got == want and got != 1 + 3 * s
+    # fp32 rounding of v: bias 2^10 and scale 2^-20 need more than 24 bits
+    words = np.array([[0x1]], dtype=np.int64)
+    v = oquant.dequantize(words, [[2.0 ** -20]], [[1024.0]], 16, 2)[0, 0]
+    assert v == 1024.0  # 1024 + 2^-20 rounds to 1024 in fp32
+
+
+@pytest.mark.parametrize("dname", ["bfloat16", "float16"])
+def test_quant_closed_form_discriminates_weight_rounding(dname):
+    """The closed-form quantized inputs the GPU tests use: the oracle's exact
+    product equals x @ v.T for the fp32 weights, and a planted mistake --
+    weights rounded to the element type before the product -- changes many
+    outputs, so a kernel that rounds them cannot pass the bitwise test."""
+    from oracle import quant as oquant
+
+    from helpers import closed_form_quant
+
+    dt = {"bfloat16": torch.bfloat16, "float16": torch.float16}[dname]
+    for bits in (2, 4, 8):
+        x, w, s, b, exact = closed_form_quant(8, 64, 256, 32, bits, dt, 3 + bits)
+        xs, ss, bs = (t.float().numpy().astype(np.float64) for t in (x, s, b))
+        got = oquant.qgemm_f64(xs, w.numpy(), ss, bs, 32, bits)
+        assert (got == exact).all()
+        want = obits.round_f32_to(exact.astype(np.float32), dname)
+        assert (obits.round_f32_to(got.astype(np.float32), dname) == want).all()
+        vt = oquant.dequantize_to(w.numpy(), ss, bs, 32, bits, dname)
+        planted = obits.round_f32_to((xs @ vt.T).astype(np.float32), dname)
+        assert (planted != want).mean() > 0.2, bits
