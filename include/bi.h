@@ -130,12 +130,13 @@ int bi_sdpa(const void* q, const void* k, const void* v,
  *   bits in {2, 4, 8}; group_size in {32, 64, 128} and dividing K.
  *
  * As in the reference kernel (a float B tile, _gemm.py:46, :170-173), v is
- * not rounded to the element type: each product x * v reaches the fp32
- * accumulator exactly for bf16 (v as three bf16 planes) and to 2^-22 |v| for
- * f16 (two f16 planes, the second scaled by 2^11 into its own chain), in a
- * fixed order per 32-element chunk of K; the output is rounded once. Nothing
- * depends on M or on a row's batch neighbours. BI_F32 activations return
- * BI_EUNSUPPORTED.
+ * not rounded to the element type. The product is formed per group in fp32:
+ * P = sum x_k * q_k and X = sum x_k over the group's 32-element chunks of K
+ * (MFMAs with exact products), then acc = fma(scale, P, acc) and
+ * acc = fma(bias, X, acc), groups in ascending order; the output is rounded
+ * once. This is sum_k x_k * v_k with fp32 roundings only, the same sequence
+ * for every output element: nothing depends on M or on a row's batch
+ * neighbours. BI_F32 activations return BI_EUNSUPPORTED.
  */
 int bi_qgemm(const void* x, const void* w, const void* scales, const void* biases, void* out,
              int64_t M, int64_t N, int64_t K, int group_size, int bits, int dtype,

@@ -153,10 +153,10 @@ extern "C" int bi_gemm_with_geometry(const void* a, const void* b, const void* b
 
 namespace {
 
-KernelFn select_qkernel(int dtype, int g, int bits) {
+KernelFn select_qkernel(int dtype, int g, int bits, int group) {
   switch (dtype) {
-    case BI_F16: return bi_qgemm_kernel_f16(g, bits);
-    case BI_BF16: return bi_qgemm_kernel_bf16(g, bits);
+    case BI_F16: return bi_qgemm_kernel_f16(g, bits, group);
+    case BI_BF16: return bi_qgemm_kernel_bf16(g, bits, group);
   }
   return nullptr;
 }
@@ -225,7 +225,7 @@ int qlaunch(const void* x, const void* w, const void* scales, const void* biases
   p.qgroup_shift = group_shift(group_size);
   const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
   if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_qgemm: too many tiles");
-  KernelFn fn = select_qkernel(dtype, g, bits);
+  KernelFn fn = select_qkernel(dtype, g, bits, group_size);
   if (!fn) return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: geometry %d not built", g);
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * G.waves), 0,
                      static_cast<hipStream_t>(stream), p);

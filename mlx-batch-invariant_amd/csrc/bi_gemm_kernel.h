@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "bi_internal.h"
 
 namespace bi_gemm_dev {
@@ -179,11 +181,13 @@ struct Slot {
   uint4* a;
   uint4* b;
 };
-// One stage of the quantized kernel's two-slot ring: the A tile and the B
-// tile's 16-bit planes (the third is unused for f16).
+// One stage of the quantized kernel's two-slot ring: the A tile, the B tile
+// (codes as element-type integers) and the stage's scale/bias entries.
 struct QSlot {
   uint4* a;
-  uint4* b[3];
+  uint4* b;
+  unsigned short* s16;
+  unsigned short* z16;
 };
 
 template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, int QB = 0>
@@ -490,33 +494,50 @@ struct GemmTile {
 
   // ---- Affine-quantized B (QB bits per weight; 16-bit elements only).
   // Weight element k of row n is bits QB * (k % (32 / QB)) of uint32 word
-  // k / (32 / QB) of that row (little-endian packing). It dequantizes to the
-  // fp32 value v = fp32(scale * q + bias) with the scale and bias of group
-  // k / group (scale * q is exact in fp32, so v has one rounding), and v enters
-  // the product in fp32. The MFMAs take 16-bit operands, so v is written to LDS
-  // as 16-bit planes whose products with the activation are exact in fp32:
-  //   bf16: v = h1 + h2 + h3, each the top 8 significant bits of what is left
-  //         (truncation, so every subtraction is exact and h3 is a bf16);
-  //         x * h1, x * h2, x * h3 accumulate into one fp32 chain, in that
-  //         order, in each chunk-step.
-  //   f16:  h1 = f16(v) (RNE), h2 = f16((v - h1) * 2^11); x * h1 and x * h2
-  //         accumulate into two chains that the epilogue joins as
-  //         fma(2^-11, chain_2, chain_1). h1 + 2^-11 h2 equals v to within
-  //         2^-22 |v| (2^-36 absolute for |v| < 2^-14, below f16's normal range).
+  // k / (32 / QB) of that row (little-endian packing) and stands for
+  // v = scale * q + bias with the scale and bias of its group k / group. The
+  // product with the activation row x is formed per group, in fp32:
+  //   P = sum_{k in group} x_k * q_k   (q_k as an element-type integer; exact
+  //                                     products, fp32 MFMA sums)
+  //   X = sum_{k in group} x_k         (the same MFMA against ones)
+  //   acc = fma(scale, P, acc); acc = fma(bias, X, acc)
+  // over groups in ascending order, acc starting at +0.0; P and X run the
+  // group's chunk-steps (32 elements of K each, the dense kernel's lane
+  // layout) from +0.0. That is sum_k x_k * (scale * q_k + bias) with fp32
+  // roundings only -- the reference's fp32 product with its fp32 weights to
+  // within fp32 accumulation error -- and a fixed sequence per output element.
   static constexpr int QP = NW == 8 ? 2 : 4;  // stages of loads in flight (registers)
-  static constexpr bool QBF16 = IsBF16<T>::value;
-  static constexpr int QPL = QBF16 ? 3 : 2;   // 16-bit planes per weight
-  static constexpr int QACC = QBF16 ? 1 : 2;  // fp32 chains per output element
+  static constexpr int GPS = EPS / 32;        // most groups that end in one stage
+  static constexpr int QSB = BN * GPS;        // scale/bias entries staged per stage
+  static constexpr int LSB = (QSB + NT - 1) / NT;
+  // B is loaded in units of CPT consecutive chunks of a row: one aligned
+  // dword (2 and 4 bits) or dword pair (8 bits) per unit.
+  static constexpr int CPT = QB == 2 ? 2 : 1;  // (1 for the dense kernels, QB = 0)
+  static constexpr int RCU = RC / CPT;        // units per tile row per stage
+  static constexpr int B_U = BN * RCU;        // units per stage
+  static constexpr int LBU = (B_U + NT - 1) / NT;
   static_assert(QB == 0 || (TB && sizeof(T) == 2 && (QB == 2 || QB == 4 || QB == 8)),
                 "quantized B: (N, K) layout, 16-bit elements, 2/4/8 bits");
+  static_assert(RC % CPT == 0, "stage holds whole units");
+  // Staged loads are kept exactly as loaded -- no arithmetic on them, not
+  // even a zero extension -- until the stage is stored: any would make the
+  // wave wait for every load in flight, the prefetched stages with them.
+  using QWord = typename std::conditional<QB == 8, uint2, uint32_t>::type;
   struct QStage {
     uint4 a[LA];
-    uint2 w[LB];     // packed bits of the 8 weights of B chunk i
-    uint32_t sz[LB];  // scale (low half) and bias (high half) of that chunk, element bits
+    QWord w[LBU];                     // packed codes of unit i
+    unsigned short sc[LSB], zb[LSB];  // scale and bias of entry i, element bits
   };
   __amdgpu_buffer_rsrc_t rs_src, rz_src;
   int64_t qrow_bytes;
   int qgshift;
+  // Per-thread load addressing, fixed for the whole K loop: byte offsets of
+  // the thread's A chunks, B units and scale/bias entries for stage 0, and
+  // the K index (or group within the stage) that decides whether a load is
+  // inside the operand. Stage s adds s * EPS elements (s * EPS * QB / 8 bytes
+  // of B, glo(s) groups).
+  uint32_t qa_off[LA], qb_off[LBU], qs_off[LSB];
+  int32_t qa_k[LA], qb_k[LBU], qs_gi[LSB];
 
   __device__ __forceinline__ void init_buffers_q(const GemmArgs& p) {
     constexpr int64_t E = sizeof(T);
@@ -528,42 +549,56 @@ struct GemmTile {
     const int64_t G = K >> qgshift;  // groups per row
     rs_src = make_rsrc(static_cast<const T*>(p.qs) + n0 * G, rows * G * E);
     rz_src = make_rsrc(static_cast<const T*>(p.qz) + n0 * G, rows * G * E);
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+      const int q = tid + i * NT, r = q / RC, c = q % RC;
+      qa_off[i] = (uint32_t)((r * K + c * EPC) * E);
+      qa_k[i] = (A_CH % NT == 0 || q < A_CH) ? c * EPC : INT32_MAX;
+    }
+#pragma unroll
+    for (int i = 0; i < LBU; i++) {
+      const int q = tid + i * NT, r = q / RCU, c = (q % RCU) * CPT;
+      qb_off[i] = (uint32_t)(r * qrow_bytes + c * EPC * QB / 8);
+      qb_k[i] = (B_U % NT == 0 || q < B_U) ? c * EPC : INT32_MAX;
+    }
+#pragma unroll
+    for (int i = 0; i < LSB; i++) {
+      const int e = tid + i * NT, r = e / GPS, gi = e % GPS;
+      qs_off[i] = (uint32_t)((r * G + gi) * E);
+      qs_gi[i] = (QSB % NT == 0 || e < QSB) ? gi : INT32_MAX;
+    }
   }
+
+  // Groups ending in stage s: [glo(s), glo(s + 1)). Stage and group sizes are
+  // powers of two, so one divides the other.
+  __device__ __forceinline__ int64_t glo(int64_t s) const { return (s * EPS) >> qgshift; }
 
   __device__ __forceinline__ void qload(int64_t s, QStage& st) const {
     constexpr uint32_t E = sizeof(T);
-    const int64_t k0 = s * EPS;
+    const int32_t kleft = (int32_t)(K - s * EPS);  // K elements from this stage on
+    const uint32_t a_step = (uint32_t)(s * EPS) * E;
+    const uint32_t b_step = (uint32_t)(s * EPS) * QB / 8;
 #pragma unroll
-    for (int i = 0; i < LA; i++) {
-      const int q = tid + i * NT;
-      if (A_CH % NT == 0 || q < A_CH) {
-        const int r = q / RC, c = q % RC;
-        const int64_t k = k0 + c * EPC;
-        st.a[i] = buffer_chunk(ra_src, k < K ? (uint32_t)((r * K + k) * E) : kOutOfRange);
-      }
+    for (int i = 0; i < LA; i++)
+      st.a[i] = buffer_chunk(ra_src, qa_k[i] < kleft ? qa_off[i] + a_step : kOutOfRange);
+#pragma unroll
+    for (int i = 0; i < LBU; i++) {
+      const uint32_t wo = qb_k[i] < kleft ? qb_off[i] + b_step : kOutOfRange;
+      if constexpr (QB == 8)
+        st.w[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rb_src, (int)wo, 0, 0));
+      else
+        st.w[i] = __builtin_amdgcn_raw_buffer_load_b32(rb_src, (int)wo, 0, 0);
     }
-    const int64_t G = K >> qgshift;
+    const int64_t g0 = glo(s);
+    const int32_t gn = (int32_t)(glo(s + 1) - g0);  // groups ending in this stage
+    const int32_t gleft = (int32_t)((K >> qgshift) - g0);
+    const uint32_t s_step = (uint32_t)g0 * E;
 #pragma unroll
-    for (int i = 0; i < LB; i++) {
-      const int q = tid + i * NT;
-      if (B_CH % NT == 0 || q < B_CH) {
-        const int r = q / RC, c = q % RC;
-        const int64_t k = k0 + c * EPC;  // first of the chunk's 8 weights
-        const bool in = k < K;
-        const uint32_t wo = in ? (uint32_t)(r * qrow_bytes + k * QB / 8) : kOutOfRange;
-        if constexpr (QB == 8) {
-          const auto v = __builtin_amdgcn_raw_buffer_load_b64(rb_src, (int)wo, 0, 0);
-          st.w[i] = __builtin_bit_cast(uint2, v);
-        } else if constexpr (QB == 4) {
-          st.w[i] = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(rb_src, (int)wo, 0, 0), 0u);
-        } else {
-          st.w[i] = make_uint2(__builtin_amdgcn_raw_buffer_load_b16(rb_src, (int)wo, 0, 0), 0u);
-        }
-        const uint32_t go = in ? (uint32_t)((r * G + (k >> qgshift)) * E) : kOutOfRange;
-        const uint32_t sc = __builtin_amdgcn_raw_buffer_load_b16(rs_src, (int)go, 0, 0);
-        const uint32_t zb = __builtin_amdgcn_raw_buffer_load_b16(rz_src, (int)go, 0, 0);
-        st.sz[i] = sc | (zb << 16);
-      }
+    for (int i = 0; i < LSB; i++) {
+      const bool in = qs_gi[i] < gn && qs_gi[i] < gleft;
+      const uint32_t go = in ? qs_off[i] + s_step : kOutOfRange;
+      st.sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs_src, (int)go, 0, 0);
+      st.zb[i] = __builtin_amdgcn_raw_buffer_load_b16(rz_src, (int)go, 0, 0);
     }
   }
 
@@ -571,28 +606,36 @@ struct GemmTile {
     return Elem<T>::to_f32(__builtin_bit_cast(T, (unsigned short)b16));
   }
 
-  // The 16-bit planes of one fp32 weight (low halves of e[0..QPL-1]).
-  __device__ __forceinline__ static void split_planes(float v, uint32_t (&e)[3]) {
-    if constexpr (QBF16) {
-      const uint32_t h1 = __float_as_uint(v) & 0xFFFF0000u;
-      const float r = v - __uint_as_float(h1);
-      const uint32_t h2 = __float_as_uint(r) & 0xFFFF0000u;
-      const uint32_t h3 = __float_as_uint(r - __uint_as_float(h2));
-      e[0] = h1 >> 16;
-      e[1] = h2 >> 16;
-      e[2] = h3 >> 16;
-    } else {
-      const _Float16 h1 = (_Float16)v;
-      const float r = v - (float)h1;
-      const _Float16 h2 = (_Float16)(r * 2048.0f);
-      e[0] = __builtin_bit_cast(unsigned short, h1);
-      e[1] = __builtin_bit_cast(unsigned short, h2);
-      e[2] = 0;
-    }
+  // Two integer codes (0 .. 255, exact in bf16 and f16) as a packed pair of
+  // element-type values, low half first.
+  __device__ __forceinline__ static uint32_t pack_codes(float c0, float c1) {
+    if constexpr (IsBF16<T>::value)  // the top halves of the fp32 values (exact: <= 8 bits)
+      return __builtin_amdgcn_perm(__float_as_uint(c1), __float_as_uint(c0), 0x07060302u);
+    else
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(c0, c1));
   }
 
-  // Stage st into LDS: A as loaded, B dequantized into its QPL planes (each in
-  // the dense (N, K) tile layout).
+  // Codes of unit st.w[i] spread one per byte: byte b of d[j] holds code
+  // b * SPREAD + j (2 and 4 bits), or byte b of word j holds code 4 j + b (8 bits).
+  static constexpr int SPREAD = (QB == 8 || QB == 0) ? 1 : 8 / QB;
+  static constexpr int ND = QB == 8 ? 2 : SPREAD;
+  __device__ __forceinline__ static void spread_codes(QWord w, uint32_t (&d)[ND]) {
+    if constexpr (QB == 8) {
+      d[0] = w.x;
+      d[1] = w.y;
+    } else {
+      constexpr uint32_t M = QB == 4 ? 0x0F0F0F0Fu : 0x03030303u;
+#pragma unroll
+      for (int j = 0; j < ND; j++) d[j] = (w >> (QB * j)) & M;
+    }
+  }
+  __device__ __forceinline__ static float code_at(const uint32_t (&d)[ND], int i) {
+    const int j = QB == 8 ? i / 4 : i % SPREAD, b = QB == 8 ? i % 4 : i / SPREAD;
+    return (float)((d[j] >> (8 * b)) & 0xFFu);  // v_cvt_f32_ubyte<b>
+  }
+
+  // Stage st into LDS: A as loaded, B's codes as element-type integers in the
+  // dense (N, K) tile layout, and the stage's scale/bias entries.
   __device__ __forceinline__ void qstore(QSlot sl, const QStage& st) const {
 #pragma unroll
     for (int i = 0; i < LA; i++) {
@@ -602,76 +645,137 @@ struct GemmTile {
         sl.a[r * RC + (c ^ swz_k(r))] = st.a[i];
       }
     }
-    constexpr uint32_t MASK = (1u << QB) - 1u;
 #pragma unroll
-    for (int i = 0; i < LB; i++) {
+    for (int i = 0; i < LBU; i++) {
       const int q = tid + i * NT;
-      if (B_CH % NT == 0 || q < B_CH) {
-        const int r = q / RC, c = q % RC;
-        const float sc = bits_to_f32(st.sz[i] & 0xFFFFu);
-        const float zb = bits_to_f32(st.sz[i] >> 16);
-        uint32_t e[8][3];
+      if (B_U % NT == 0 || q < B_U) {
+        const int r = q / RCU, c = (q % RCU) * CPT;
+        uint32_t d[ND];
+        spread_codes(st.w[i], d);
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-          const uint32_t word = (QB == 8 && t >= 4) ? st.w[i].y : st.w[i].x;
-          const int sh = QB == 8 ? 8 * (t & 3) : QB * t;
-          const float qv = (float)((word >> sh) & MASK);
-          split_planes(__builtin_fmaf(sc, qv, zb), e[t]);
-        }
-        const int at = r * RC + (c ^ swz_k(r));
-#pragma unroll
-        for (int pl = 0; pl < QPL; pl++) {
+        for (int cc = 0; cc < CPT; cc++) {
           uint4 v;
-          v.x = e[0][pl] | (e[1][pl] << 16);
-          v.y = e[2][pl] | (e[3][pl] << 16);
-          v.z = e[4][pl] | (e[5][pl] << 16);
-          v.w = e[6][pl] | (e[7][pl] << 16);
-          sl.b[pl][at] = v;
+          v.x = pack_codes(code_at(d, 8 * cc + 0), code_at(d, 8 * cc + 1));
+          v.y = pack_codes(code_at(d, 8 * cc + 2), code_at(d, 8 * cc + 3));
+          v.z = pack_codes(code_at(d, 8 * cc + 4), code_at(d, 8 * cc + 5));
+          v.w = pack_codes(code_at(d, 8 * cc + 6), code_at(d, 8 * cc + 7));
+          sl.b[r * RC + ((c + cc) ^ swz_k(r))] = v;
         }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < LSB; i++) {
+      const int e = tid + i * NT;
+      if (QSB % NT == 0 || e < QSB) {
+        sl.s16[e] = st.sc[i];
+        sl.z16[e] = st.zb[i];
       }
     }
   }
 
-  // Chunk-step j of the stage in `sl` for every block of this wave.
-  __device__ __forceinline__ void q_step(QSlot sl, int j, f32x4_t (&acc)[QACC][FM][FN]) const {
-    uint4 av[FM];
+  // Fold group gi of the stage in `sl` (its scale and bias per column) into
+  // acc; with `restart`, P and X start over from +0.0 (otherwise the next
+  // group's first chunk-step starts them).
+  __device__ __forceinline__ void q_fold(QSlot sl, int gi, bool restart, f32x4_t (&acc)[FM][FN],
+                                         f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
 #pragma unroll
-    for (int i = 0; i < FM; i++) av[i] = sl.a[a_off[j] + i * 16 * RC];
-#pragma unroll
-    for (int pl = 0; pl < QPL; pl++) {
-      uint4 bv[FN];
-#pragma unroll
-      for (int jn = 0; jn < FN; jn++) bv[jn] = sl.b[pl][b_off[j] + jn * 16 * RC];
+    for (int jn = 0; jn < FN; jn++) {
+      const int at = (wn * WTN + jn * 16 + r16) * GPS + gi;
+      const float sc = bits_to_f32(sl.s16[at]), zb = bits_to_f32(sl.z16[at]);
 #pragma unroll
       for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int jn = 0; jn < FN; jn++) {
-          f32x4_t& c = acc[QBF16 ? 0 : pl][i][jn];
-          c = chunk_step(T(0), av[i], bv[jn], c);
+        for (int e = 0; e < 4; e++) {
+          acc[i][jn][e] = __builtin_fmaf(sc, P[i][jn][e], acc[i][jn][e]);
+          acc[i][jn][e] = __builtin_fmaf(zb, X[i][e], acc[i][jn][e]);
         }
     }
-  }
-
-  __device__ __forceinline__ void q_compute(QSlot sl, int steps,
-                                            f32x4_t (&acc)[QACC][FM][FN]) const {
-    if (steps == CS) {
+    if (restart) {
 #pragma unroll
-      for (int j = 0; j < CS; j++) q_step(sl, j, acc);
-    } else {
+      for (int i = 0; i < FM; i++) {
+        X[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < CS - 1; j++)
-        if (j < steps) q_step(sl, j, acc);
+        for (int jn = 0; jn < FN; jn++) P[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
     }
   }
 
-  // Loads run QP stages ahead in registers; each stage is dequantized into
-  // one of two LDS slots one stage before it is computed (whole rounds of QP
+  // One chunk-step into P and X; `first` (the group's first chunk-step)
+  // starts them from +0.0.
+  __device__ __forceinline__ void q_mfma(const uint4 (&av)[FM], const uint4 (&bv)[FN], bool first,
+                                         f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
+    constexpr uint32_t ONE = IsBF16<T>::value ? 0x3F803F80u : 0x3C003C00u;
+    const uint4 ones = make_uint4(ONE, ONE, ONE, ONE);
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      X[i] = chunk_step(T(0), av[i], ones, first ? zero : X[i]);
+#pragma unroll
+      for (int jn = 0; jn < FN; jn++)
+        P[i][jn] = chunk_step(T(0), av[i], bv[jn], first ? zero : P[i][jn]);
+    }
+  }
+
+  // All CS chunk-steps of stage s (held in `sl`), operands of step j + 1 read
+  // while step j's MFMAs run; a group that ends inside the stage is folded
+  // right after its last chunk-step. GS (the group size) is a compile-time
+  // constant, so the fold positions are too.
+  template <int GS>
+  __device__ __forceinline__ void q_compute_full(QSlot sl, int64_t s, f32x4_t (&acc)[FM][FN],
+                                                 f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
+    constexpr int CPG = GS / 32;  // chunk-steps per group
+    uint4 av[2][FM], bv[2][FN];
+    read_operands(Slot{sl.a, sl.b}, 0, av[0], bv[0]);
+#pragma unroll
+    for (int j = 0; j < CS; j++) {
+      if (j + 1 < CS) read_operands(Slot{sl.a, sl.b}, j + 1, av[(j + 1) & 1], bv[(j + 1) & 1]);
+      // Inside a stage, a group starts at every CPG-th chunk-step when
+      // groups are no longer than stages; longer groups restart at the fold.
+      q_mfma(av[j & 1], bv[j & 1], GS <= EPS && j % CPG == 0, P, X);
+      if constexpr (GS <= EPS) {
+        if ((j + 1) % CPG == 0) q_fold(sl, (j + 1) / CPG - 1, false, acc, P, X);
+      }
+    }
+    if constexpr (GS > EPS) {
+      if ((((s + 1) * EPS) & (GS - 1)) == 0) q_fold(sl, 0, true, acc, P, X);
+    }
+  }
+
+  // The first `steps` (< CS) chunk-steps of the last stage.
+  template <int GS>
+  __device__ __forceinline__ void q_compute_part(QSlot sl, int64_t s, int steps,
+                                                 f32x4_t (&acc)[FM][FN], f32x4_t (&P)[FM][FN],
+                                                 f32x4_t (&X)[FM]) const {
+#pragma unroll
+    for (int j = 0; j < CS - 1; j++) {
+      if (j < steps) {
+        uint4 av[FM], bv[FN];
+        read_operands(Slot{sl.a, sl.b}, j, av, bv);
+        const int64_t k_beg = (s * CS + j) * 32, k_end = k_beg + 32;
+        q_mfma(av, bv, (k_beg & (GS - 1)) == 0, P, X);
+        if ((k_end & (GS - 1)) == 0) q_fold(sl, (int)(k_end / GS - 1 - glo(s)), false, acc, P, X);
+      }
+    }
+  }
+
+  template <int GS>
+  __device__ __forceinline__ void q_compute(QSlot sl, int64_t s, int steps, f32x4_t (&acc)[FM][FN],
+                                            f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
+    if (steps == CS)
+      q_compute_full<GS>(sl, s, acc, P, X);
+    else if (steps > 0)
+      q_compute_part<GS>(sl, s, steps, acc, P, X);
+  }
+
+  // Loads run QP stages ahead in registers; each stage is converted into one
+  // of two LDS slots one stage before it is computed (whole rounds of QP
   // stages, so ring indices are compile-time). Before a slot is rewritten,
   // the barrier guarantees every wave finished reading it (LDS reads retire
   // before the barrier: lgkmcnt(0)).
-  template <bool COMPUTE, typename QSlots>
+  template <bool COMPUTE, int GS, typename QSlots>
   __device__ __forceinline__ void q_rounds(const QSlots& slots, int64_t nst, int64_t nsteps,
-                                           QStage (&q)[QP], f32x4_t (&acc)[QACC][FM][FN]) const {
+                                           QStage (&q)[QP], f32x4_t (&acc)[FM][FN],
+                                           f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
     for (int64_t s0 = 0; s0 < nst; s0 += QP) {
 #pragma unroll
       for (int u = 0; u < QP; u++) {
@@ -679,24 +783,32 @@ struct GemmTile {
         asm volatile("s_barrier" ::: "memory");
         qstore(slots((u + 1) & 1), q[(u + 1) % QP]);
         qload(s0 + u + 1 + QP, q[(u + 1) % QP]);
-        if constexpr (COMPUTE) q_compute(slots(u & 1), steps_of(nsteps, s0 + u), acc);
+        if constexpr (COMPUTE)
+          q_compute<GS>(slots(u & 1), s0 + u, steps_of(nsteps, s0 + u), acc, P, X);
       }
     }
   }
 
-  template <typename QSlots>
+  template <int GS, typename QSlots>
   __device__ __forceinline__ void main_loop_q(const QSlots& slots, int64_t nst, int64_t nsteps,
-                                              bool computes, f32x4_t (&acc)[QACC][FM][FN]) const {
+                                              bool computes, f32x4_t (&acc)[FM][FN]) const {
     static_assert(QP % 2 == 0, "ring of two LDS slots");
+    f32x4_t P[FM][FN], X[FM];
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      X[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jn = 0; jn < FN; jn++) P[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
     QStage q[QP];
 #pragma unroll
     for (int u = 0; u < QP; u++) qload(u, q[u]);
     qstore(slots(0), q[0]);
     qload(QP, q[0]);
     if (computes)
-      q_rounds<true>(slots, nst, nsteps, q, acc);
+      q_rounds<true, GS>(slots, nst, nsteps, q, acc, P, X);
     else
-      q_rounds<false>(slots, nst, nsteps, q, acc);
+      q_rounds<false, GS>(slots, nst, nsteps, q, acc, P, X);
   }
 
   // Register-staged path (unaligned operands): two slots, double buffered.
@@ -809,22 +921,22 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
   }
 }
 
-// Quantized-B GEMM: the dense kernel's tile walk and chunk-step order, with B
-// dequantized to fp32 and held as 16-bit planes (GemmTile's quantized part).
-// Every output element sees, per chunk-step, the planes' MFMAs in a fixed
-// order on its own row of A and column of B; the footprint only decides which
-// elements a workgroup owns. Epilogue: bf16 acc, f16 fma(2^-11, chain_2,
-// chain_1); then one RNE rounding.
-template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int QB>
+// Quantized-B GEMM: the dense kernel's tile walk and chunk-step order over
+// B's integer codes, with the per-group scale and bias folded into the fp32
+// accumulator (GemmTile's quantized part). Every output element sees the same
+// sequence of MFMAs and folds on its own row of A and column of B; the
+// footprint only decides which elements a workgroup owns. One RNE rounding at
+// the end.
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int QB, int GS>
 __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
   using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, 2, true, QB>;
-  constexpr int FM = Tile::FM, FN = Tile::FN, QACC = Tile::QACC, QPL = Tile::QPL;
-  constexpr int AC = Tile::A_CH, BC = Tile::B_CH, BC3 = QPL > 2 ? BC : 1;
-  __shared__ uint4 a0[AC], p00[BC], p01[BC], p02[BC3];
-  __shared__ uint4 a1[AC], p10[BC], p11[BC], p12[BC3];
+  constexpr int FM = Tile::FM, FN = Tile::FN;
+  constexpr int AC = Tile::A_CH, BC = Tile::B_CH, SB = Tile::QSB;
+  __shared__ uint4 a0[AC], b0[BC], a1[AC], b1[BC];
+  __shared__ unsigned short s0[SB], z0[SB], s1[SB], z1[SB];
   auto slots = [&](int u) -> QSlot {
-    if (u == 0) return {a0, {p00, p01, p02}};
-    return {a1, {p10, p11, p12}};
+    if (u == 0) return {a0, b0, s0, z0};
+    return {a1, b1, s1, z1};
   };
 
   Tile t;
@@ -850,18 +962,16 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
   const int64_t wrow = t.m0 + t.wm * Tile::WTM, wcol = t.n0 + t.wn * Tile::WTN;
   const bool computes = t.wave < Tile::CW && wrow < M && wcol < N;
 
-  f32x4_t acc[QACC][FM][FN];
+  f32x4_t acc[FM][FN];
 #pragma unroll
-  for (int ch = 0; ch < QACC; ch++)
+  for (int i = 0; i < FM; i++)
 #pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int jn = 0; jn < FN; jn++) acc[ch][i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int jn = 0; jn < FN; jn++) acc[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   t.init_lds_offsets();
   // The host launches quantized kernels only with 16-byte aligned rows of A.
   t.init_buffers_q(p);
-  t.main_loop_q(slots, nst, nsteps, computes, acc);
+  t.template main_loop_q<GS>(slots, nst, nsteps, computes, acc);
 
   if (!computes) return;
   T* __restrict__ out = static_cast<T*>(p.out);
@@ -874,11 +984,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int64_t row = wrow + i * 16 + 4 * t.g + e;
-        if (row < M) {
-          float v = acc[0][i][jn][e];
-          if constexpr (QACC == 2) v = __builtin_fmaf(0x1p-11f, acc[QACC - 1][i][jn][e], v);
-          out[row * N + col] = Elem<T>::from_f32(v);
-        }
+        if (row < M) out[row * N + col] = Elem<T>::from_f32(acc[i][jn][e]);
       }
     }
   }
@@ -911,19 +1017,29 @@ KernelFn kernel_for(int g, bool trans_b) {
 }
 
 // Quantized-B kernel for geometry g (16-bit element types; (N, K) packed B).
-// Two LDS slots of A plus the B planes; the 256 x 128 footprint would need
-// 160 KB of LDS and is not built.
+// The 256 x 128 footprint is not built: with the loads in flight in
+// registers it would spill.
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int QB>
+KernelFn qkernel_gs(int group) {
+  switch (group) {
+    case 32: return gemm_qkernel<T, BM, BN, WM, WN, NW, KB, QB, 32>;
+    case 64: return gemm_qkernel<T, BM, BN, WM, WN, NW, KB, QB, 64>;
+    case 128: return gemm_qkernel<T, BM, BN, WM, WN, NW, KB, QB, 128>;
+  }
+  return nullptr;
+}
+
 template <typename T>
-KernelFn qkernel_for(int g, int bits) {
-#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns)                       \
-  case id:                                                                 \
-    if constexpr (bm * bn <= 128 * 128) {                                  \
-      switch (bits) {                                                      \
-        case 2: return gemm_qkernel<T, bm, bn, wm, wn, nw, kb, 2>;         \
-        case 4: return gemm_qkernel<T, bm, bn, wm, wn, nw, kb, 4>;         \
-        case 8: return gemm_qkernel<T, bm, bn, wm, wn, nw, kb, 8>;         \
-      }                                                                    \
-    }                                                                      \
+KernelFn qkernel_for(int g, int bits, int group) {
+#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns)                                \
+  case id:                                                                          \
+    if constexpr (bm * bn <= 128 * 128) {                                           \
+      switch (bits) {                                                               \
+        case 2: return qkernel_gs<T, bm, bn, wm, wn, nw, kb, 2>(group);             \
+        case 4: return qkernel_gs<T, bm, bn, wm, wn, nw, kb, 4>(group);             \
+        case 8: return qkernel_gs<T, bm, bn, wm, wn, nw, kb, 8>(group);             \
+      }                                                                             \
+    }                                                                               \
     return nullptr;
   switch (g) { BI_GEOMETRIES(BI_QGEO_CASE) }
 #undef BI_QGEO_CASE
@@ -936,5 +1052,5 @@ KernelFn qkernel_for(int g, int bits) {
 bi_gemm_dev::KernelFn bi_gemm_kernel_f32(int g, bool trans_b);
 bi_gemm_dev::KernelFn bi_gemm_kernel_f16(int g, bool trans_b);
 bi_gemm_dev::KernelFn bi_gemm_kernel_bf16(int g, bool trans_b);
-bi_gemm_dev::KernelFn bi_qgemm_kernel_f16(int g, int bits);
-bi_gemm_dev::KernelFn bi_qgemm_kernel_bf16(int g, int bits);
+bi_gemm_dev::KernelFn bi_qgemm_kernel_f16(int g, int bits, int group);
+bi_gemm_dev::KernelFn bi_qgemm_kernel_bf16(int g, int bits, int group);

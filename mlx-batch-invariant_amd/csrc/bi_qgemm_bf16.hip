@@ -2,6 +2,6 @@
 // instantiations compile in parallel with the dense ones).
 #include "bi_gemm_kernel.h"
 
-bi_gemm_dev::KernelFn bi_qgemm_kernel_bf16(int g, int bits) {
-  return bi_gemm_dev::qkernel_for<__bf16>(g, bits);
+bi_gemm_dev::KernelFn bi_qgemm_kernel_bf16(int g, int bits, int group) {
+  return bi_gemm_dev::qkernel_for<__bf16>(g, bits, group);
 }

@@ -36,10 +36,19 @@ DEVICE_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# The quantized kernels fold each group's MFMA sums into the accumulator with
+# VALU arithmetic; with the MFMA results in accumulation registers every fold
+# would copy them out and back. This keeps MFMA operands and results in VGPRs.
+EXTRA_FLAGS = {
+    "bi_qgemm_f16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "bi_qgemm_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *DEVICE_FLAGS, "-I", INCLUDE, "-I", HERE, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [HIPCC, *DEVICE_FLAGS, *EXTRA_FLAGS.get(src, []), "-I", INCLUDE, "-I", HERE, "-c",
+           os.path.join(HERE, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd[cmd.index("-c"):cmd.index("-c")] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

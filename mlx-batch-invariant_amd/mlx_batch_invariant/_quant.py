@@ -13,13 +13,13 @@ word ``k // (32 / bits)`` of row n (little-endian packing). ``scales`` and
 uint32 arithmetic, so packed words are held in int32 tensors (same bits);
 uint32 is accepted too.
 
-Arithmetic, as the reference's kernel (_gemm.py:170-173 into a float B tile):
-each weight dequantizes to the fp32 value ``v = fp32(scale * q + bias)`` and
-enters the product unrounded; accumulation is fp32 and the output is rounded
-once. The kernel feeds v to 16-bit MFMAs as planes whose products are exact
-(bf16: three planes, exact; f16: two, to 2^-22 |v|), in a fixed order per
-chunk of K, so invariance holds exactly as for the dense GEMM. Note that
-:func:`dequantize` returns v rounded to the element type (what
+Arithmetic: the reference's kernel (_gemm.py:170-173, into a float B tile)
+multiplies by the fp32 value ``v = scale * q + bias`` and accumulates in
+fp32. The kernel here forms the same sum per group, ``scale * sum(x * q) +
+bias * sum(x)``, with exact products in its MFMAs and fp32 roundings only, in
+a fixed order per element, so invariance holds exactly as for the dense GEMM
+and the result is within fp32 accumulation error of the reference's. Note
+that :func:`dequantize` returns v rounded to the element type (what
 ``mx.dequantize`` returns); ``linear(x, dequantize(w))`` therefore differs from
 ``quantized_linear`` by that rounding of the weights.
 """

@@ -8,9 +8,10 @@ dequantize  -- reference _gemm.py:170-173: v = float(scale) * float(q) +
                significant bits), so v has one rounding. The reference keeps v
                in fp32: it is stored to a float B tile (_gemm.py:46, :80) and
                enters the product unrounded.
-qgemm_f64   -- the exact value the reference's quantized GEMM approximates:
-               float64 x @ v.T (x has at most 11 significant bits and v 24, so
-               every product is exact in float64).
+qgemm_f64   -- the exact value the reference's quantized GEMM approximates
+               with fp32 arithmetic: float64 x @ v.T (x has at most 11
+               significant bits and v 24, so every product is exact in
+               float64).
 
 Pinned in tests/test_oracle.py by hand-worked words (known answers), a planted
 big-endian packing mistake, and closed-form weights whose fp32 values are not

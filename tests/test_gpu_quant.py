@@ -2,12 +2,12 @@
 _gemm.py:159-177 and 243-285; tests/test_invariance.py:477-592).
 
 Parity: the reference dequantizes each weight to an fp32 value v and
-multiplies in fp32 (its B tile is float). The kernel does the same -- every
-product x * v reaches the fp32 accumulator exactly (bf16) or to 2^-22 |v|
-(f16) -- so on inputs whose products and partial sums are exact in fp32 its
-result is the exact product rounded once, bit for bit, and on random inputs
-it is within 1 ULP of the exact product (the dense GEMM's bound). The oracle
-is oracle/quant.py, pinned in tests/test_oracle.py.
+multiplies in fp32 (its B tile is float). The kernel forms the same sum per
+group as scale * sum(x q) + bias * sum(x), with exact products and fp32
+roundings only, so on inputs whose partial sums are exact in fp32 its result
+is the exact product rounded once, bit for bit, and on random inputs it is
+within 1 ULP of the exact product with the fp32 weights (the dense GEMM's
+bound). The oracle is oracle/quant.py, pinned in tests/test_oracle.py.
 """
 
 import numpy as np
@@ -53,10 +53,11 @@ def _launch(L, x, q, s, b, gs, nbits, g):
 @pytest.mark.parametrize("nbits", [2, 4, 8])
 def test_closed_form_products_are_exact(cuda, dname, dtype, nbits):
     """Weights whose fp32 values are not representable in the element type and
-    small-integer activations: the result is the exact product rounded once,
-    bitwise. A kernel that rounded the weights to the element type first
-    fails this (tests/test_oracle.py shows the planted rounding changes >20%
-    of these outputs)."""
+    small-integer activations (every partial sum a multiple of 2^-11 below
+    2^13): the result is the exact product rounded once, bitwise. A kernel
+    that rounded the weights to the element type first fails this
+    (tests/test_oracle.py shows the planted rounding changes >20% of these
+    outputs)."""
     for gs in (32, 64, 128):
         for M, N, K in [(1, 48, 256), (19, 64, 512), (70, 130, 384)]:
             x, q, s, b, exact = closed_form_quant(M, N, K, gs, nbits, dtype, 100 + nbits + gs + M)
