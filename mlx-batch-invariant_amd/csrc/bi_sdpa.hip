@@ -33,6 +33,8 @@
 #include <atomic>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "bi_internal.h"
 
 namespace {
@@ -57,6 +59,14 @@ struct SdpaArgs {
 };
 
 template <typename T> __device__ inline float to_f32(T x) { return (float)x; }
+// A mask element held as its zero-extended bits (16-bit types) or as itself
+// (fp32).
+template <typename T, typename R> __device__ inline float raw_to_f32(R x) {
+  if constexpr (sizeof(T) == 4)
+    return x;
+  else
+    return (float)__builtin_bit_cast(T, (unsigned short)x);
+}
 template <typename T> __device__ inline T from_f32(float x) { return (T)x; }  // RNE
 
 template <int CTRL>
@@ -88,6 +98,16 @@ __device__ inline void load_raw(const T* __restrict__ row, int r, uint4* dst) {
 #pragma unroll
   for (int i = 0; i < NC; i++)
     dst[i] = *reinterpret_cast<const uint4*>(row + (r + kGroupLanes * i) * CE);
+}
+
+// Emits nothing, but the values count as produced here and memory accesses
+// may not move across: they are computed before any later load is issued.
+template <int NE>
+__device__ inline void settle(float* x) {
+  static_assert(NE % 4 == 0, "groups of four");
+#pragma unroll
+  for (int e = 0; e < NE; e += 4)
+    asm volatile("" : "+v"(x[e]), "+v"(x[e + 1]), "+v"(x[e + 2]), "+v"(x[e + 3]) :: "memory");
 }
 
 template <typename T, int NC>
@@ -168,37 +188,65 @@ __global__ void __launch_bounds__(kThreads) sdpa_kernel(SdpaArgs p) {
   if (p.mask_mode == BI_MASK_ARRAY)
     mbase = static_cast<const T*>(p.mask) + b * p.ms[0] + h0 * p.ms[1] + s * p.ms[2];
 
-  // Key i of this partial: the raw chunks of the PF keys ahead live in kq/vq.
+  // Key i of this partial: the raw chunks (and raw mask values) of the PF
+  // keys ahead live in kq/vq/mq. Loads are unconditional -- a key past the
+  // last usable one reloads that key, and its values go unused -- and stay
+  // untouched until the key is used: a load under a branch, or arithmetic on
+  // a loaded register right after it is issued, would make the wave wait for
+  // every load in flight, the prefetched keys included.
+  // Mask elements: 16-bit ones are held zero-extended in a register of their
+  // own (two in one register would need a merge that waits for the load).
+  using MRaw = typename std::conditional<sizeof(T) == 4, float, unsigned short>::type;
+  using MReg = typename std::conditional<sizeof(T) == 4, float, uint32_t>::type;
+  const MRaw* __restrict__ mraw = reinterpret_cast<const MRaw*>(mbase);
+  const int64_t klast = kend - 1;
   uint4 kq[PF][NCK], vq[PF][NCV];
+  MReg mq[PF][GC];
+  if (kend > 0) {
 #pragma unroll
-  for (int u = 0; u < PF; u++) {
-    const int64_t i = part + (int64_t)kPartials * u;
-    if (i < kend) {
+    for (int u = 0; u < PF; u++) {
+      const int64_t i0 = part + (int64_t)kPartials * u;
+      const int64_t i = i0 < klast ? i0 : klast;
       load_raw<T, D>(kb + i * p.ks[2], r, kq[u]);
       load_raw<T, V>(vb + i * p.vs[2], r, vq[u]);
+      if (mraw) {
+#pragma unroll
+        for (int g = 0; g < GC; g++) mq[u][g] = mraw[g * p.ms[1] + i];
+      }
     }
   }
   for (int64_t i0 = part; i0 < kend; i0 += (int64_t)kPartials * PF) {
 #pragma unroll
     for (int u = 0; u < PF; u++) {
       const int64_t i = i0 + (int64_t)kPartials * u;
+      float kf[EQ], vf[EV], mv[GC];
+      to_floats<T, NCK>(kq[u], kf);
+      to_floats<T, NCV>(vq[u], vf);
+      if (mraw) {
+#pragma unroll
+        for (int g = 0; g < GC; g++) mv[g] = raw_to_f32<T>(mq[u][g]);
+      }
+      // Finish converting before the reload below is issued: converted lazily
+      // after it, the old and new raw values would need two register sets
+      // and a copy that waits for the reload.
+      settle<EQ>(kf);
+      settle<EV>(vf);
+      const int64_t in0 = i + (int64_t)kPartials * PF;
+      const int64_t inext = in0 < klast ? in0 : klast;
+      load_raw<T, D>(kb + inext * p.ks[2], r, kq[u]);
+      load_raw<T, V>(vb + inext * p.vs[2], r, vq[u]);
+      if (mraw) {
+#pragma unroll
+        for (int g = 0; g < GC; g++) mq[u][g] = mraw[g * p.ms[1] + inext];
+      }
       if (i < kend) {
-        float kf[EQ], vf[EV];
-        to_floats<T, NCK>(kq[u], kf);
-        to_floats<T, NCV>(vq[u], vf);
-        const int64_t inext = i + (int64_t)kPartials * PF;
-        if (inext < kend) {
-          load_raw<T, D>(kb + inext * p.ks[2], r, kq[u]);
-          load_raw<T, V>(vb + inext * p.vs[2], r, vq[u]);
-        }
 #pragma unroll
         for (int g = 0; g < GC; g++) {
           float bias2 = 0.f;
           bool use = true;
-          if (mbase) {
-            const float mv = to_f32<T>(mbase[g * p.ms[1] + i]);
-            use = mv > -3.0e38f;
-            bias2 = mv * kLog2e;
+          if (mraw) {
+            use = mv[g] > -3.0e38f;
+            bias2 = mv[g] * kLog2e;
           }
           if (use) {
             float d = 0.f;
@@ -210,8 +258,15 @@ __global__ void __launch_bounds__(kThreads) sdpa_kernel(SdpaArgs p) {
             const float pe = __builtin_amdgcn_exp2f(sc - nm);
             m[g] = nm;
             l[g] = __builtin_fmaf(l[g], f, pe);
+            // o * f is o exactly when f == 1 (the running max did not move,
+            // the usual case after the first keys): skipping the product
+            // then changes no bits.
+            if (f != 1.f) {
 #pragma unroll
-            for (int e = 0; e < EV; e++) o[g][e] = __builtin_fmaf(pe, vf[e], o[g][e] * f);
+              for (int e = 0; e < EV; e++) o[g][e] = o[g][e] * f;
+            }
+#pragma unroll
+            for (int e = 0; e < EV; e++) o[g][e] = __builtin_fmaf(pe, vf[e], o[g][e]);
           }
         }
       }
