@@ -36,6 +36,7 @@
 #include <type_traits>
 
 #include "bi_internal.h"
+#include "bi_sdpa_args.h"
 
 namespace {
 
@@ -43,20 +44,6 @@ constexpr int kThreads = 256;
 constexpr int kPartials = 32;
 constexpr int kGroupLanes = 8;
 constexpr float kLog2e = 1.4426950408889634f;
-
-struct SdpaArgs {
-  const void* q;
-  const void* k;
-  const void* v;
-  const void* mask;
-  const void* sinks;
-  void* out;
-  int64_t B, H, Hkv, qL, N;
-  int64_t qs[3], ks[3], vs[3], ms[3];  // element strides for (b, h, s|n)
-  float scale2;                        // scale * log2(e)
-  int mask_mode;
-  int64_t causal_offset;
-};
 
 template <typename T> __device__ inline float to_f32(T x) { return (float)x; }
 // A mask element held as its zero-extended bits (16-bit types) or as itself
@@ -399,6 +386,7 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
   const int64_t rows = B * H * qL;
   if (rows == 0) return BI_OK;
   if (rows > INT32_MAX) return bi::fail(BI_EINVAL, "bi_sdpa: B*H*qL too large");
+  if (N > INT32_MAX - 1024) return bi::fail(BI_EINVAL, "bi_sdpa: N=%lld keys is too many", (long long)N);
   const int gc = heads_per_group(H / Hkv, D, rows);
   SdpaFn fn = select_kernel(dtype, D, V, gc);
   const int64_t blocks = rows / gc;
@@ -440,8 +428,11 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
   p.mask_mode = mask_mode;
   p.causal_offset = mask_mode == BI_MASK_CAUSAL ? causal_offset : 0;
 
-  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(hip_stream), p);
+  // bf16 and f16 run on matrix cores (bi_sdpa_mfma.hip); fp32 on the VALU
+  // kernel above. Each is the only arithmetic for its element type.
+  if (!sdpa_mfma_launch(p, dtype, D, device_cus(), static_cast<hipStream_t>(hip_stream)))
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(hip_stream), p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return bi::launch_error(e, "bi_sdpa launch");
   return BI_OK;

@@ -20,7 +20,7 @@ BUILD = os.path.join(PKG_ROOT, "_build")
 LIB = os.path.join(PKG_ROOT, "mlx_batch_invariant", "libbi.so")
 
 SOURCES = ["bi_abi.cpp", "bi_gemm.hip", "bi_gemm_f32.hip", "bi_gemm_f16.hip", "bi_gemm_bf16.hip",
-           "bi_qgemm_f16.hip", "bi_qgemm_bf16.hip", "bi_sdpa.hip"]
+           "bi_qgemm_f16.hip", "bi_qgemm_bf16.hip", "bi_sdpa.hip", "bi_sdpa_mfma.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -36,12 +36,14 @@ DEVICE_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-# The quantized kernels fold each group's MFMA sums into the accumulator with
-# VALU arithmetic; with the MFMA results in accumulation registers every fold
-# would copy them out and back. This keeps MFMA operands and results in VGPRs.
+# The quantized GEMM and the MFMA attention work on MFMA results with VALU
+# arithmetic (group folds; softmax and rescaling); with the results in
+# accumulation registers every such step would copy them out and back. This
+# keeps MFMA operands and results in VGPRs.
 EXTRA_FLAGS = {
     "bi_qgemm_f16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "bi_qgemm_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "bi_sdpa_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

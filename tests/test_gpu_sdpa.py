@@ -77,10 +77,11 @@ def test_batch_invariance(cuda):
 @pytest.mark.parametrize("H,Hkv,D,batches", [(32, 8, 128, (1, 32, 64)),
                                               (32, 4, 64, (1, 32, 64, 128))])
 def test_head_grouping_does_not_change_bits(cuda, H, Hkv, D, batches):
-    """Large grids let one workgroup serve several query heads of a GQA group
-    (sharing their key and value loads); small grids give each head its own
-    workgroup. The batch sizes here cross both choices: a row's bits must not
-    move."""
+    """The launch shape follows the grid: bf16/f16 decode batches that fill
+    the GPU give each wave all output dims of its query columns, smaller ones
+    split the dims over waves and workgroups (the fp32 kernel likewise groups
+    query heads per workgroup by grid size). The batch sizes here cross those
+    choices: a row's bits must not move."""
     N = 256
     for dname, dtype in DTYPES:
         q1 = rn((1, H, 1, D), dtype, 31, device=cuda)
