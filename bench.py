@@ -11,6 +11,10 @@ resident in HBM. Alongside, on the same run:
     duration measured with HIP events on the launch stream;
   * stock torch.matmul (hipBLASLt) on the same inputs, interleaved;
   * decode SDPA (configs[2]: B = 64, 32/8 heads, D = 128, N = 8192) GB/s;
+  * causal prefill SDPA (B = 1, 32/8 heads, D = 128, 2048 x 2048) TFLOP/s,
+    against stock torch SDPA;
+  * 4-bit affine quantized linear (4096 x 4096, group 64) at M = 1 and 256,
+    against stock dequantize + F.linear;
   * a bit-invariance check of one row across batch sizes 1..256;
   * the CPU baseline: the oracle's fixed-order fp32 restatement of the
     reference GEMM (C, OpenMP) on a bounded sample of the same workload.
@@ -259,6 +263,34 @@ def main():
                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(sbytes / sd_bi / 1e3 / PEAK_HBM_GBS, 4)}}
 
+    # Causal prefill attention (the query-row-blocked path of the same kernel):
+    # B=1, 32/8 heads, D=128, 2048 query rows over 2048 keys.
+    L = 2048
+    qp = torch.randn(1, H, L, D, generator=g).to(torch.bfloat16).to(dev)
+    kp = torch.randn(1, Hkv, L, D, generator=g).to(torch.bfloat16).to(dev)
+    vp = torch.randn(1, Hkv, L, D, generator=g).to(torch.bfloat16).to(dev)
+    pf_bi = statistics.median(time_us(lambda: bi.scaled_dot_product_attention(
+        qp, kp, vp, scale=sc, mask="causal"), reps=5) for _ in range(5))
+    pf_st = statistics.median(time_us(lambda: torch.nn.functional.scaled_dot_product_attention(
+        qp, kp, vp, scale=sc, is_causal=True, enable_gqa=True), reps=5) for _ in range(5))
+    pf_flops = 4 * H * L * L * D / 2  # QK^T and PV over the causal half
+    prefill = {"config": dict(B=1, H=H, Hkv=Hkv, qL=L, N=L, D=D, mask="causal", dtype="bf16"),
+               "bi_us": round(pf_bi, 1), "bi_tflops": round(pf_flops / pf_bi / 1e6, 1),
+               "stock_us": round(pf_st, 1), "stock_tflops": round(pf_flops / pf_st / 1e6, 1)}
+
+    # Affine 4-bit quantized linear (group 64), 4096 x 4096 weight: decode and
+    # M=256 rows; stock is dequantize + F.linear.
+    wq = (torch.randn(4096, 4096, generator=g) / 64).to(torch.bfloat16)
+    qw, qs, qz = (t.to(dev) for t in bi.quantize(wq, 64, 4))
+    quant = {"config": dict(N=4096, K=4096, bits=4, group_size=64, dtype="bf16")}
+    for Mq in (1, 256):
+        xq = torch.randn(Mq, 4096, generator=g).to(torch.bfloat16).to(dev)
+        q_bi = statistics.median(time_us(lambda: bi.quantized_linear(xq, qw, qs, qz, 64, 4))
+                                 for _ in range(5))
+        q_st = statistics.median(time_us(lambda: torch.nn.functional.linear(
+            xq, bi.dequantize(qw, qs, qz, 64, 4))) for _ in range(5))
+        quant["M%d" % Mq] = {"bi_us": round(q_bi, 1), "stock_us": round(q_st, 1)}
+
     # Invariance spot check: row 0 of the (4096, 4096) shape across batch sizes.
     a, w = ops[1][2], ops[1][3]
     ref = bits(bi.matmul(a[:1].contiguous(), w)[0])
@@ -280,6 +312,8 @@ def main():
         "cpu_baseline": cpu,
         "per_shape": per_shape,
         "sdpa_decode": sdpa,
+        "sdpa_prefill": prefill,
+        "quantized_linear": quant,
         "invariance_bits_differing_batch_1_to_256": differing,
         "model_determinism": model,
         "device": torch.cuda.get_device_name(0),
