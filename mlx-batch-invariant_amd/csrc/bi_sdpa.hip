@@ -1,4 +1,6 @@
-// Batch-invariant single-pass scaled dot product attention for gfx950.
+// Batch-invariant single-pass scaled dot product attention for gfx950: the
+// fp32 kernel (bf16 and f16 run on matrix cores, bi_sdpa_mfma.hip), and the
+// C entry point bi_sdpa that validates arguments and launches either.
 //
 // Restates the reference bi_sdpa (mlx_batch_invariant/_attention.py:32-149):
 // one workgroup owns the whole reduction over the key sequence for a query
@@ -352,14 +354,9 @@ SdpaFn kernel_for_dims(int64_t D, int64_t V, int gc) {
   return nullptr;
 }
 
-SdpaFn select_kernel(int dtype, int64_t D, int64_t V, int gc) {
-  switch (dtype) {
-    case BI_F32: return kernel_for_dims<float>(D, V, gc);
-    case BI_F16: return kernel_for_dims<_Float16>(D, V, gc);
-    case BI_BF16: return kernel_for_dims<__bf16>(D, V, gc);
-  }
-  return nullptr;
-}
+// The head dims built for every element type (fp32 here, bf16 / f16 in
+// bi_sdpa_mfma.hip).
+bool dims_built(int64_t D, int64_t V) { return D == V && (D == 64 || D == 128 || D == 256); }
 
 }  // namespace
 
@@ -380,16 +377,13 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
     return bi::fail(BI_EINVAL, "bi_sdpa: unknown mask mode %d", mask_mode);
   if (mask_mode == BI_MASK_ARRAY && (!mask || !mask_strides))
     return bi::fail(BI_EINVAL, "bi_sdpa: array mask needs a mask pointer and strides");
-  if (!select_kernel(dtype, D, V, 1))
+  if (!dims_built(D, V))
     return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: head dims D=%lld V=%lld are not built "
                     "(supported: D == V in {64, 128, 256})", (long long)D, (long long)V);
   const int64_t rows = B * H * qL;
   if (rows == 0) return BI_OK;
   if (rows > INT32_MAX) return bi::fail(BI_EINVAL, "bi_sdpa: B*H*qL too large");
   if (N > INT32_MAX - 1024) return bi::fail(BI_EINVAL, "bi_sdpa: N=%lld keys is too many", (long long)N);
-  const int gc = heads_per_group(H / Hkv, D, rows);
-  SdpaFn fn = select_kernel(dtype, D, V, gc);
-  const int64_t blocks = rows / gc;
   if (!q || !out || (N > 0 && (!k || !v)))
     return bi::fail(BI_EINVAL, "bi_sdpa: null tensor pointer");
 
@@ -428,11 +422,25 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
   p.mask_mode = mask_mode;
   p.causal_offset = mask_mode == BI_MASK_CAUSAL ? causal_offset : 0;
 
-  // bf16 and f16 run on matrix cores (bi_sdpa_mfma.hip); fp32 on the VALU
-  // kernel above. Each is the only arithmetic for its element type.
-  if (!sdpa_mfma_launch(p, dtype, D, device_cus(), static_cast<hipStream_t>(hip_stream)))
-    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), 0,
+  // The MFMA kernel addresses 32 key / value rows from a block's first row
+  // with 32-bit byte offsets.
+  if (dtype != BI_F32) {
+    const int64_t st = p.ks[2] > p.vs[2] ? p.ks[2] : p.vs[2];
+    if ((32 * st + D) * esz > INT32_MAX)
+      return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: key/value row stride %lld is too large",
+                      (long long)st);
+  }
+  // fp32 runs on the VALU kernel above; bf16 and f16 on matrix cores
+  // (bi_sdpa_mfma.hip). Each is the only arithmetic for its element type.
+  if (dtype == BI_F32) {
+    const int gc = heads_per_group(H / Hkv, D, rows);
+    SdpaFn fn = kernel_for_dims<float>(D, V, gc);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(rows / gc)), dim3(kThreads), 0,
                        static_cast<hipStream_t>(hip_stream), p);
+  } else if (!sdpa_mfma_launch(p, dtype, D, device_cus(), static_cast<hipStream_t>(hip_stream))) {
+    return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: no MFMA kernel for dtype %d D=%lld", dtype,
+                    (long long)D);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return bi::launch_error(e, "bi_sdpa launch");
   return BI_OK;

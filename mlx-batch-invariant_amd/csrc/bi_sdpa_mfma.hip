@@ -5,32 +5,36 @@
 // its query columns -- a column is one (query head, query row) pair; the
 // columns of a workgroup share a batch index and a kv head, so they read the
 // same keys and values -- with no split-KV, no second pass and no switch on
-// query length or context length. Which columns share a workgroup, and where
-// a column sits in it, never changes the column's arithmetic.
+// query length or context length. The workgroup's 4 waves walk the keys in a
+// fixed stride order (the reference's fixed per-simdgroup strides, :89) and
+// their partial results are merged in a fixed order through LDS (:124-141).
 //
 // Fixed per-column arithmetic (the invariance contract):
-//   * Keys are consumed in blocks of 32 (keys 32b .. 32b + 31), ascending.
+//   * Keys are taken in blocks of 32 (block b = keys 32b .. 32b + 31). Block b
+//     belongs to chain b mod 4; each chain walks its blocks in ascending order.
 //   * Score: raw_i = q . k_i as a chain of v_mfma_f32_16x16x32_{bf16,f16}
 //     over the head dim in ascending 32-element chunks from +0.0 (exact
 //     products, fp32 sums); s_i = raw_i * (scale * log2 e), plus
 //     mask_i * log2 e for an additive mask.
 //   * Key i is used iff i < N, i <= row + causal_offset (causal) and
 //     mask_i > -3e38 (array mask) (reference :92-96).
-//   * Online softmax in base 2, one chain per column over the blocks: with M
-//     the largest used score of the block (none: the block leaves the column
+//   * Each chain runs an online softmax in base 2 over its blocks: with M the
+//     largest used score of the block (none: the block leaves the chain
 //     unchanged), m' = max(m, M), f = m' == m ? 1 : exp2(m - m'),
 //     p_i = exp2(s_i - m') (0 for unused keys), l = fma(l, f, sum_i p_i) with
-//     the block sum taken in a fixed tree; o = o * f (skipped when f == 1,
-//     which changes no bits), then o += p . v as v_mfma_f32_16x16x16 with p
+//     the block sum taken in a fixed tree; o = o * f + 0.0 (skipped when
+//     f == 1, which changes no bits), then o += p . v as v_mfma_f32_16x16x16 with p
 //     split into hi = T(p) and lo = T(p - hi): for each 16-dim block, keys
 //     0-15 hi, keys 0-15 lo, keys 16-31 hi, keys 16-31 lo. m starts at the
-//     lowest finite float and l at 0; a sink starts them at
-//     sink * log2 e and 1 (reference :80-86).
-//   * out = l == 0 ? o : o / l, one rounding to T.
-// Every column, whatever workgroup, wave or lane it lands in and however many
-// rows or heads share its keys, runs exactly this sequence: an output row has
-// the same bits for any batch, query length, context past its visible keys,
-// and launch shape.
+//     lowest finite float and l at 0; a sink starts chain 0 at m =
+//     sink * log2 e, l = 1 (reference :80-86).
+//   * Merge: M = max over the chains' m; for c = 0, 1, 2, 3 in order,
+//     e_c = exp2(m_c - M), L = fma(l_c, e_c, L) and O = fma(o_c, e_c, O) from
+//     L = O = +0.0; out = L == 0 ? O : O / L, one rounding to T.
+// Every column, whatever workgroup or lane it lands in, however many rows or
+// heads share its keys and whatever the launch shape (columns per workgroup,
+// prefetch depths), runs exactly this sequence: an output row has the same
+// bits for any batch, query length and context past its visible keys.
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <math.h>
@@ -46,8 +50,10 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // 16-byte copies as single vector loads / stores (a uint4 assignment is a
 // struct copy, which would keep staged data in scratch memory).
@@ -58,13 +64,25 @@ __device__ __forceinline__ void st16(uint4* p, uint4 v) {
   *reinterpret_cast<u32x4_t*>(p) = __builtin_bit_cast(u32x4_t, v);
 }
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // = chains
 constexpr int kThreads = 64 * kWaves;
-constexpr int kCols = 16 * kWaves;  // query columns per workgroup
-constexpr int kBlk = 32;            // keys per block
+constexpr int kBlk = 32;   // keys per block
 constexpr float kLog2e = 1.4426950408889634f;
-// s_waitcnt immediate (gfx9 encoding): vmcnt 63 (no wait), expcnt 7, lgkmcnt 0.
-constexpr int kWaitLdsOnly = 0xF | (0x3 << 14) | (0x7 << 4);
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4],
+// lgkmcnt [11:8]).
+constexpr int lcm(int a, int b) {
+  int x = a, y = b;
+  while (y) {
+    const int t = x % y;
+    x = y;
+    y = t;
+  }
+  return a / x * b;
+}
+constexpr int wait_vm(int vm) { return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int kWaitAll = 0;
+constexpr int kWaitLds = 0xF | (0x3 << 14) | (0x7 << 4);  // lgkmcnt(0) only
 
 // 16x16x32: lane (r = lane % 16, g = lane / 16) supplies A[r][8g + t] and
 // B[8g + t][r], t = 0..7; it receives C[4g + e][r], e = 0..3.
@@ -87,17 +105,41 @@ __device__ inline f32x4_t mma16(_Float16, uint2 a, uint2 b, f32x4_t c) {
                                                __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
 }
 
+// ds_read_b64_tr_b16 (in each 16-lane group, lane i receives element i of
+// the four 4 x 16-bit rows its group addresses, one per row) as an asm
+// statement. Values arrive in LDS through loads that write it directly; the
+// compiler's tracking of those loads cannot always tell which slot an
+// intrinsic read touches and then waits for every load in flight, including
+// the next blocks' prefetch. As asm the read is ordered by the explicit waits
+// only: the caller waits for the slot's loads before and for the read
+// (lgkmcnt) after.
+__device__ __forceinline__ u32x2_t ds_read_tr(uint32_t lds_addr) {
+  u32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(lds_addr) : "memory");
+  return v;
+}
+
 template <typename T> __device__ inline unsigned short tbits(T x) {
   return __builtin_bit_cast(unsigned short, x);
-}
-template <typename T> __device__ inline float tval(unsigned short b) {
-  return (float)__builtin_bit_cast(T, b);
 }
 
 __device__ inline int xcd_remap(int w, int total) {
   const int per = total >> 3;
   if (w < (per << 3)) return (w & 7) * per + (w >> 3);
   return w;
+}
+
+// Buffer resource over [base, base + bytes) (wave-uniform): loads past the
+// end return zeros without touching memory.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  constexpr int64_t kMax = 0x7FFFFFFF;
+  const int32_t n = bytes <= 0 ? 0 : (int32_t)(bytes < kMax ? bytes : kMax);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, __builtin_amdgcn_readfirstlane(n),
+                                           0x00020000);
 }
 
 // Sum / max over the four lanes of a column (lanes r, r + 16, r + 32, r + 48,
@@ -117,134 +159,128 @@ __device__ inline float half_pair(float x, bool is_max) {
 __device__ inline float col_sum(float x) { return half_pair(row_pair(x, false), false); }
 __device__ inline float col_max(float x) { return half_pair(row_pair(x, true), true); }
 
-// Launch shape: CT column tiles of 16 columns per workgroup; the 4 / CT waves
-// of a column tile split its output dims, NB 16-dim blocks each, so a
-// workgroup covers DW = (4 / CT) * NB * 16 dims and D / DW workgroups share a
-// column tile's dims. Waves that share a column tile compute its scores and
-// softmax statistics identically. The shape changes which wave does what,
-// never a column's arithmetic.
-template <typename T, int D, int CT, int NB>
-struct Attn {
-  static constexpr int DS = kWaves / CT;           // waves per column tile
-  static constexpr int DW = DS * NB * 16;          // output dims per workgroup
-  static constexpr int WS = D / DW;                // workgroups per column tile
-  static constexpr int CH = D / 8;                 // 16-byte chunks per key row
-  static constexpr int VCH = DW / 8;               // value chunks per row held
-  static constexpr int NQ = D / 32;                // score MFMAs per 16 keys
-  static constexpr int SB = D == 256 ? 1 : 2;      // blocks per stage (one barrier)
-  static constexpr int SK = SB * kBlk;             // keys per stage
-  static constexpr int KCH = SK * CH;              // chunks per K tile
-  static constexpr int VTCH = SK * VCH;            // chunks per V tile
-  static constexpr int LK = KCH / kThreads;        // K chunks per thread per stage
-  static constexpr int LV = (VTCH + kThreads - 1) / kThreads;
-  static constexpr int QP = 2;                     // stages of loads in flight
-  static_assert(QP % 2 == 0, "the two LDS slots alternate within a round of QP stages");
-  static_assert(KCH % kThreads == 0 && D % DW == 0 && NB >= 1, "shape");
+// Launch shape: CT column tiles of 16 columns per workgroup, shared by the 4
+// waves (one chain each); WS workgroups split a column tile's output dims
+// (each computes the same scores and statistics, and o for D / WS dims); a
+// wave's keys are loaded PK blocks ahead into the score MFMAs' registers and
+// its values SV - 1 blocks ahead into its own LDS slots. None of these
+// enters a column's arithmetic.
+template <typename T, int D, int CT, int PK, int SV, int WS>
+struct Chain {
+  static constexpr int NQ = D / 32;            // score MFMAs per 16 keys
+  static constexpr int DW = D / WS;            // output dims per workgroup
+  static constexpr int NB = DW / 16;           // 16-dim blocks of o held
+  static constexpr int VCH = DW / 8;           // 16-byte chunks per value row held
+  static constexpr int NKL = 2 * NQ;           // key loads per block per lane
+  static constexpr int DV = kBlk * VCH / 64;   // value LDS-DMA loads per block
+  static constexpr int VSLOT = kBlk * VCH;     // uint4 per value slot
+  static constexpr int ARR_U4 = kWaves * VSLOT;  // one slot of every wave
+  // Value reads as asm statements (see ds_read_tr) except with 8 value loads
+  // per block, where the compiler's own waits before the intrinsic read were
+  // checked to be exactly VWAIT and it schedules the products among the reads.
+  static constexpr bool ASM_TR = DV != 8;
+  // Vector-memory operations issued after a block's value loads and before
+  // its values are read: at least those of the SV - 1 blocks issued since
+  // (the prologue issues the first SV - 1 value blocks before the first PK
+  // key blocks, which keeps the count when PK >= SV - 2).
+  static constexpr int VWAIT = (SV - 1) * (NKL + DV);
+  static_assert(SV >= 2 && SV <= 6 && PK >= 0 && PK >= SV - 2 && D % (16 * WS) == 0 && VCH >= 2,
+                "shape");
+  static_assert(VWAIT <= 63, "value loads in flight exceed the vmcnt range");
+  // The merge stages one column tile at a time: every chain's o fills one
+  // slot array exactly and its (m, l) fit in another.
+  static_assert(kWaves * NB * 64 == ARR_U4 && kWaves * 64 / 2 <= ARR_U4, "merge staging");
 
-  // K tile: [SK keys][CH chunks], chunk c of key r at c ^ swz_k(r): the score
-  // MFMA's A reads (16 keys, one chunk each) then hit distinct banks.
-  __device__ __forceinline__ static int swz_k(int r) { return r & ((CH < 16 ? CH : 16) - 1); }
-  // V tile: [SK keys][VCH chunks] read transposed by ds_read_tr16_b64 (four
-  // consecutive keys, 32 bytes each): rows k .. k + 3 land on distinct banks.
+  // Value slot: [32 keys][VCH chunks], chunk c of key r at c ^ swz_v(r):
+  // ds_read_tr16_b64 reads four consecutive keys of 16 dims, and the swizzle
+  // puts those rows on distinct banks.
   __device__ __forceinline__ static int swz_v(int r) {
     return ((((r & 3) << 1) | (((r >> 3) & 1) << 3))) & (VCH - 1);
   }
 
-  struct Stage {
-    uint4 k[LK], v[LV];
-  };
-  struct Slot {
-    uint4* k;
-    uint4* v;
-  };
-
+  // Key and value rows of the stream. Each block's buffer resources start at
+  // the block's first row, so the lane offsets are the same for every block
+  // (and below 2^31: the host bounds 32 * stride); loads for blocks i >= nit
+  // use an empty resource, which reads nothing and returns zeros.
   const T* kb;
-  const T* vb;  // first of this workgroup's value dims
-  int64_t ks2, vs2;
-  int klast, tid;
+  const T* vb;
+  int64_t ks2, vs2, N, nit;
+  int wave;
+  uint32_t koff[2][NQ], voff[DV];
 
-  // Loads of stage s (keys past the last usable one reload it: the values
-  // go unused). Loaded registers are left untouched until stored.
-  __device__ __forceinline__ void load(int64_t s, Stage& st) const {
+  __device__ __forceinline__ void init(const SdpaArgs& p, int64_t b, int64_t kvh, int ws, int w,
+                                       int64_t n_it, int lane) {
+    constexpr uint32_t E = sizeof(T);
+    const int g = lane >> 4, r16 = lane & 15;
+    kb = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
+    vb = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];  // row starts
+    ks2 = p.ks[2];
+    vs2 = p.vs[2];
+    N = p.N;
+    nit = n_it;
+    wave = w;
 #pragma unroll
-    for (int i = 0; i < LK; i++) {
-      const int q = tid + i * kThreads, r = q / CH, c = q % CH;
-      int key = (int)s * SK + r;
-      key = key < klast ? key : klast;
-      st.k[i] = ld16(kb + (int64_t)key * ks2 + c * 8);
-    }
+    for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-    for (int i = 0; i < LV; i++) {
-      const int q = tid + i * kThreads;
-      if (VTCH % kThreads == 0 || q < VTCH) {
-        const int r = q / VCH, c = q % VCH;
-        int key = (int)s * SK + r;
-        key = key < klast ? key : klast;
-        st.v[i] = ld16(vb + (int64_t)key * vs2 + c * 8);
-      }
+      for (int i = 0; i < NQ; i++)
+        koff[kt][i] = (uint32_t)(((16 * kt + r16) * ks2 + 32 * i + 8 * g) * E);
+#pragma unroll
+    for (int j = 0; j < DV; j++) {
+      const int pos = j * 64 + lane, r = pos / VCH, c = (pos % VCH) ^ swz_v(r);
+      voff[j] = (uint32_t)((r * vs2 + ws * DW + c * 8) * E);
     }
   }
-  __device__ __forceinline__ void store(Slot sl, const Stage& st) const {
-#pragma unroll
-    for (int i = 0; i < LK; i++) {
-      const int q = tid + i * kThreads, r = q / CH, c = q % CH;
-      st16(sl.k + r * CH + (c ^ swz_k(r)), st.k[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < LV; i++) {
-      const int q = tid + i * kThreads;
-      if (VTCH % kThreads == 0 || q < VTCH) {
-        const int r = q / VCH, c = q % VCH;
-        st16(sl.v + r * VCH + (c ^ swz_v(r)), st.v[i]);
-      }
-    }
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const T* base, int64_t stride,
+                                                         int64_t i) const {
+    const int64_t key0 = (wave + kWaves * i) * kBlk;
+    const bool in = i < nit;
+    return make_rsrc(base + (in ? key0 * stride : 0),
+                     in ? ((N - key0 - 1) * stride + D) * (int64_t)sizeof(T) : 0);
   }
-
-  __device__ __forceinline__ void prologue(Stage (&st)[QP], Slot first) const {
+  // Keys of block i into the score MFMAs' A operands: lane (r16, g) holds
+  // K[16kt + r16][32q + 8g .. + 7].
+  __device__ __forceinline__ void kload(int64_t i, uint4 (&kr)[2][NQ]) const {
+    const auto rs = rsrc(kb, ks2, i);
 #pragma unroll
-    for (int u = 0; u < QP; u++) load(u, st[u]);
-    store(first, st[0]);
-    load(QP, st[0]);
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int q = 0; q < NQ; q++)
+        kr[kt][q] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)koff[kt][q], 0, 0));
   }
-
-  // Stages s0 .. s0 + QP - 1: before computing stage s0 + u from one LDS
-  // slot, stage s0 + u + 1 (loaded QP stages earlier) is stored to the other
-  // and stage s0 + u + 1 + QP is loaded in its registers.
-  template <typename Slots, typename Compute>
-  __device__ __forceinline__ void round(int64_t s0, Stage (&st)[QP], const Slots& slots,
-                                        const Compute& compute) const {
+  // Values of block i into an LDS slot (loads that write LDS directly).
+  __device__ __forceinline__ void vload(int64_t i, uint4* dst) const {
+    const auto rs = rsrc(vb, vs2, i);
+    // The slot's previous reads have returned before new values land.
+    __builtin_amdgcn_s_waitcnt(kWaitLds);
 #pragma unroll
-    for (int u = 0; u < QP; u++) {
-      // LDS writes and reads of the previous block retired, then the
-      // barrier; the global loads in flight are not waited for.
-      __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
-      asm volatile("s_barrier" ::: "memory");
-      store(slots((u + 1) & 1), st[(u + 1) % QP]);
-      load(s0 + u + 1 + QP, st[(u + 1) % QP]);
-      compute(slots(u & 1), s0 + u);
-    }
+    for (int j = 0; j < DV; j++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + j * 64), 16, (int)voff[j],
+                                               0, 0, 0);
   }
 };
 
-template <typename T, int D, int CT, int NB>
+template <typename T, int D, int CT, int PK, int SV, int WS>
 __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
-  using A = Attn<T, D, CT, NB>;
-  constexpr int CH = A::CH, VCH = A::VCH, NQ = A::NQ, QP = A::QP, DS = A::DS, WS = A::WS;
+  using C = Chain<T, D, CT, PK, SV, WS>;
+  constexpr int NQ = C::NQ, NB = C::NB, VCH = C::VCH;
   constexpr int COLS = 16 * CT;  // columns per workgroup
-  __shared__ uint4 k0s[A::KCH], v0s[A::VTCH], k1s[A::KCH], v1s[A::VTCH];
-  auto slots = [&](int u) __attribute__((always_inline)) -> typename A::Slot {
-    if (u == 0) return {k0s, v0s};
-    return {k1s, v1s};
+  // Value slot s of every wave is array s: an LDS read then names the one
+  // array whose loads it waits for, and loads into the other slots stay in
+  // flight.
+  __shared__ uint4 va0[C::ARR_U4], va1[C::ARR_U4], va2[SV > 2 ? C::ARR_U4 : 1],
+      va3[SV > 3 ? C::ARR_U4 : 1], va4[SV > 4 ? C::ARR_U4 : 1], va5[SV > 5 ? C::ARR_U4 : 1];
+  auto arr = [&](int s) __attribute__((always_inline)) -> uint4* {
+    return s == 0 ? va0 : s == 1 ? va1 : s == 2 ? va2 : s == 3 ? va3 : s == 4 ? va4 : va5;
   };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // the chain
   const int g = lane >> 4, r16 = lane & 15;
-  const int ct = wave % CT, ds = wave / CT;
 
   // Workgroup -> (batch, kv head, block of COLS of the G x qL columns of that
-  // kv head -- column cc is row cc / G, head cc % G -- and slice of DW dims).
+  // kv head -- column cc is row cc / G, head cc % G -- and slice of dims).
   const int64_t G = p.H / p.Hkv;
   const int64_t ncol = G * p.qL;
   const int64_t ncb = (ncol + COLS - 1) / COLS;
@@ -256,12 +292,6 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   const int64_t kvh = t % p.Hkv;
   const int64_t b = t / p.Hkv;
   const int64_t c0 = cb * COLS;
-  const int64_t cc = c0 + ct * 16 + r16;  // this lane's column
-  const bool colv = cc < ncol;
-  const int64_t srow = colv ? cc / G : 0;
-  const int64_t head = kvh * G + (colv ? cc % G : 0);
-  const bool wave_cols = c0 + ct * 16 < ncol;  // wave-uniform: any column here
-  const int dw0 = ws * A::DW + ds * NB * 16;    // first output dim of this wave
 
   // Keys of a column: [0, kend); the workgroup walks the blocks that its last
   // row can see.
@@ -271,193 +301,276 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
     return last < 0 ? 0 : (last + 1 < p.N ? last + 1 : p.N);
   };
   const int64_t last_cc = (c0 + COLS < ncol ? c0 + COLS : ncol) - 1;
-  const int64_t kmax = kend_of(last_cc / G);
-  const int kend = colv ? (int)kend_of(srow) : 0;
+  const int64_t nblk = (kend_of(last_cc / G) + kBlk - 1) / kBlk;
   const int nkeys = (int)p.N;
-  const int64_t nblk = (kmax + kBlk - 1) / kBlk;
-  const int64_t nst = (nblk + A::SB - 1) / A::SB;
+  const bool has_mask = p.mask_mode == BI_MASK_ARRAY;
 
-  // The column's query as the B operand of the score MFMAs: Q[col][32t + 8g ..].
-  uint4 qt[NQ];
-  {
-    const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + head * p.qs[1] + srow * p.qs[2];
+  // This lane's column in each tile; its query as the B operand of the score
+  // MFMAs (Q[col][32i + 8g ..]); its chain state.
+  bool colv[CT];
+  int64_t srow[CT], head[CT];
+  int kend[CT];
+  uint4 qt[CT][NQ];
+  const T* mrow[CT];
+  float m[CT], l[CT];
+  f32x4_t o[CT][NB];
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++) {
+    const int64_t cc = c0 + 16 * ct + r16;
+    colv[ct] = cc < ncol;
+    srow[ct] = colv[ct] ? cc / G : 0;
+    head[ct] = kvh * G + (colv[ct] ? cc % G : 0);
+    kend[ct] = colv[ct] ? (int)kend_of(srow[ct]) : 0;
+    const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + head[ct] * p.qs[1] + srow[ct] * p.qs[2];
 #pragma unroll
     for (int i = 0; i < NQ; i++)
-      qt[i] = colv ? ld16(qrow + 32 * i + 8 * g) : make_uint4(0, 0, 0, 0);
-  }
-  float m = -FLT_MAX, l = 0.f;
-  if (p.sinks && colv) {
-    m = (float)static_cast<const T*>(p.sinks)[head] * kLog2e;
-    l = 1.f;
-  }
-  f32x4_t o[NB];
+      qt[ct][i] = colv[ct] ? ld16(qrow + 32 * i + 8 * g) : make_uint4(0, 0, 0, 0);
+    mrow[ct] = has_mask ? static_cast<const T*>(p.mask) + b * p.ms[0] + head[ct] * p.ms[1] +
+                              srow[ct] * p.ms[2]
+                        : nullptr;
+    m[ct] = -FLT_MAX;
+    l[ct] = 0.f;
+    if (wave == 0 && p.sinks && colv[ct]) {
+      m[ct] = (float)static_cast<const T*>(p.sinks)[head[ct]] * kLog2e;
+      l[ct] = 1.f;
+    }
 #pragma unroll
-  for (int i = 0; i < NB; i++) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // Array mask row of the column (lanes without a column read the first row).
-  const bool has_mask = p.mask_mode == BI_MASK_ARRAY;
-  const T* mrow = has_mask ? static_cast<const T*>(p.mask) + b * p.ms[0] + head * p.ms[1] +
-                                 srow * p.ms[2]
-                           : nullptr;
+    for (int i = 0; i < NB; i++) o[ct][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
-  A at;
-  at.kb = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
-  at.vb = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1] + ws * A::DW;
-  at.ks2 = p.ks[2];
-  at.vs2 = p.vs[2];
-  at.klast = (int)p.N - 1;
-  at.tid = tid;
-
-  // Block blk (rows 32j .. 32j + 31 of the stage tiles in sl) for this wave's
-  // 16 columns and NB dim blocks.
-  auto compute = [&](typename A::Slot sl, int j, int64_t blk) __attribute__((always_inline)) {
+  // Key and value rows of the stream; per-block buffer resources start at the
+  // block's first row, so the lane offsets below are the same for every block
+  // (and below 2^31: the host bounds 32 * stride).
+  // This chain's blocks are wave + 4i, i < nit.
+  const int64_t nit = nblk > wave ? (nblk - wave + kWaves - 1) / kWaves : 0;
+  const int wslot = wave * C::VSLOT;  // this wave's slot within each array
+  C ld;
+  ld.init(p, b, kvh, ws, wave, nit, lane);
+  // One block of this chain: keys in kr, values in value slot `slot`.
+  auto compute = [&](const uint4 (&kr)[2][NQ], int slot, int64_t blk) __attribute__((always_inline)) {
     // Scores: S^T tiles (16 keys x 16 columns); lane (g, r16) holds keys
     // 16kt + 4g + e of column r16.
-    f32x4_t sc[2];
+    f32x4_t sc[CT][2];
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-      sc[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const int kr = kBlk * j + 16 * kt + r16;
+    for (int ct = 0; ct < CT; ct++)
 #pragma unroll
-      for (int i = 0; i < NQ; i++)
-        sc[kt] = mma32(T(0), ld16(sl.k + kr * CH + ((4 * i + g) ^ A::swz_k(kr))), qt[i], sc[kt]);
-    }
+      for (int kt = 0; kt < 2; kt++) {
+        sc[ct][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NQ; i++) sc[ct][kt] = mma32(T(0), kr[kt][i], qt[ct][i], sc[ct][kt]);
+      }
     // Key indices fit in 32 bits (the host checks N < 2^31).
     const int key0 = (int)blk * kBlk + 4 * g;
-    float s[2][4];
-    bool use[2][4];
+    uint2 ph[CT][2], pl[CT][2];
+    float f[CT];
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        s[kt][e] = sc[kt][e] * p.scale2;
-        use[kt][e] = key0 + 16 * kt + e < kend;
-      }
-    if (has_mask) {  // wave-uniform; every lane loads (in bounds), unused lanes ignore it
+    for (int ct = 0; ct < CT; ct++) {
+      float s[2][4];
+      bool use[2][4];
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const int key = key0 + 16 * kt + e;
-          const float mv = (float)mrow[key < nkeys ? key : 0];
-          use[kt][e] = use[kt][e] && mv > -3.0e38f;
-          s[kt][e] = s[kt][e] + mv * kLog2e;
+          s[kt][e] = sc[ct][kt][e] * p.scale2;
+          use[kt][e] = key0 + 16 * kt + e < kend[ct];
         }
-    }
-    float bm = -INFINITY;
+      if (has_mask) {  // wave-uniform; every lane loads (in bounds), unused lanes ignore it
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+        for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
-    bm = col_max(bm);
-    const bool any = bm > -INFINITY;
-    const float mn = any ? fmaxf(m, bm) : m;
-    const float f = mn == m ? 1.f : __builtin_amdgcn_exp2f(m - mn);
-    float pv[2][4];
-    float ps = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(s[kt][e] - mn) : 0.f;
-        ps = ps + pv[kt][e];
+          for (int e = 0; e < 4; e++) {
+            const int key = key0 + 16 * kt + e;
+            const float mv = (float)mrow[ct][key < nkeys ? key : 0];
+            use[kt][e] = use[kt][e] && mv > -3.0e38f;
+            s[kt][e] = s[kt][e] + mv * kLog2e;
+          }
       }
-    ps = col_sum(ps);
-    l = __builtin_fmaf(l, f, ps);
-    m = mn;
-    // P^T as the B operand of the 16x16x16 MFMAs, split into two planes.
-    uint2 ph[2], pl[2];
+      float bm = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-      unsigned short hb[4], lb[4];
+      for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const T hi = (T)pv[kt][e];
-        hb[e] = tbits(hi);
-        lb[e] = tbits((T)(pv[kt][e] - (float)hi));
+        for (int e = 0; e < 4; e++) bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
+      bm = col_max(bm);
+      const bool any = bm > -INFINITY;
+      const float mn = any ? fmaxf(m[ct], bm) : m[ct];
+      f[ct] = mn == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - mn);
+      float pv[2][4];
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(s[kt][e] - mn) : 0.f;
+          ps = ps + pv[kt][e];
+        }
+      ps = col_sum(ps);
+      l[ct] = __builtin_fmaf(l[ct], f[ct], ps);
+      m[ct] = mn;
+      // P^T as the B operand of the 16x16x16 MFMAs, split into two planes.
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        unsigned short hb[4], lb[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const T hi = (T)pv[kt][e];
+          hb[e] = tbits(hi);
+          lb[e] = tbits((T)(pv[kt][e] - (float)hi));
+        }
+        ph[ct][kt] = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
+        pl[ct][kt] = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
       }
-      ph[kt] = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
-      pl[kt] = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
     }
-    if (f != 1.f) {
+    // Rescale; adding +0.0 turns an underflowed -0.0 into +0.0, so o is never
+    // -0.0 and a column with no usable key in this block (f == 1, all p == 0)
+    // keeps its o exactly through the products below.
 #pragma unroll
-      for (int i = 0; i < NB; i++) o[i] = o[i] * f;
+    for (int ct = 0; ct < CT; ct++)
+      if (f[ct] != 1.f) {
+#pragma unroll
+        for (int i = 0; i < NB; i++) o[ct][i] = o[ct][i] * f[ct] + 0.f;
+      }
+    // The block's values have landed in the slot (vector memory completes in
+    // order: at most VWAIT younger operations may still be in flight).
+    __builtin_amdgcn_s_waitcnt(wait_vm(C::VWAIT));
+    asm volatile("" ::: "memory");
+    uint4* const vslot = arr(slot) + wslot;
+    u32x2_t va[NB][2];
+#pragma unroll
+    for (int db = 0; db < NB; db++) {
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        // V^T block (dims 16db .., keys 16kt + 4g ..): lane r16 addresses key
+        // 16kt + 4g + r16 / 4 at dim col and receives V[16kt + 4g + t][16db + r16].
+        const int kr = 16 * kt + 4 * g + (r16 >> 2);
+        const int col = 16 * db + 4 * (r16 & 3);
+        const int chunk = (col >> 3) ^ C::swz_v(kr);
+        const int off = (kr * VCH + chunk) * 16 + (col & 7) * 2;
+        if constexpr (C::ASM_TR) {
+          va[db][kt] = ds_read_tr((uint32_t)(uintptr_t)(lds_void_t*)vslot + off);
+        } else {
+          va[db][kt] = __builtin_bit_cast(
+              u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                           (lds_i16x4_t*)(reinterpret_cast<char*>(vslot) + off)));
+        }
+      }
     }
-    // A column with no usable key in this block keeps its o exactly (adding
-    // the zero products could still turn a -0.0 into +0.0).
-    const bool keep = colv && !any;
-    f32x4_t saved[NB];
-    const bool slow = __builtin_amdgcn_ballot_w64(keep) != 0;
-    if (slow) {
+    if constexpr (C::ASM_TR) {
+      // All of them have returned; the empty statements make every use of a
+      // read's result come after the wait.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-      for (int i = 0; i < NB; i++) saved[i] = o[i];
+      for (int db = 0; db < NB; db++) asm volatile("" : "+v"(va[db][0]), "+v"(va[db][1]));
     }
 #pragma unroll
     for (int db = 0; db < NB; db++) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
-        // V^T block (this wave's dim block db, keys 16kt + 4g ..): lane r16
-        // addresses key 16kt + 4g + r16 / 4 at tile dim col and receives
-        // V[16kt + 4g + t][col0 + r16], t = 0..3.
-        const int kr = kBlk * j + 16 * kt + 4 * g + (r16 >> 2);
-        const int col = 16 * (ds * NB + db) + 4 * (r16 & 3);
-        const int chunk = (col >> 3) ^ A::swz_v(kr);
-        const char* addr = reinterpret_cast<const char*>(sl.v) + (kr * VCH + chunk) * 16 + (col & 7) * 2;
-        const uint2 va = __builtin_bit_cast(
-            uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(addr)));
-        o[db] = mma16(T(0), va, ph[kt], o[db]);
-        o[db] = mma16(T(0), va, pl[kt], o[db]);
-      }
-    }
-    if (slow && keep) {
+        const uint2 v2 = __builtin_bit_cast(uint2, va[db][kt]);
 #pragma unroll
-      for (int i = 0; i < NB; i++) o[i] = saved[i];
+        for (int ct = 0; ct < CT; ct++) {
+          o[ct][db] = mma16(T(0), v2, ph[ct][kt], o[ct][db]);
+          o[ct][db] = mma16(T(0), v2, pl[ct][kt], o[ct][db]);
+        }
+      }
     }
   };
 
-  if (nst > 0) {
-    typename A::Stage st[QP];
-    at.prologue(st, slots(0));
-    for (int64_t s0 = 0; s0 < nst; s0 += QP)
-      at.round(s0, st, slots, [&](typename A::Slot sl, int64_t stg) __attribute__((always_inline)) {
-        if (wave_cols) {
+  // Block i of the chain: keys loaded at step i - PK, values at step
+  // i - SV + 1 into slot i % SV. The loop is unrolled over U steps (the
+  // least common multiple of the two rotations) so that register and slot
+  // indices are compile-time.
+  constexpr int U = lcm(PK + 1, SV);
+  uint4 kr[PK + 1][2][NQ];
 #pragma unroll
-          for (int j = 0; j < A::SB; j++)
-            if (stg * A::SB + j < nblk) compute(sl, j, stg * A::SB + j);
-        }
-      });
+  for (int u = 0; u < SV - 1; u++) ld.vload(u, arr(u) + wslot);
+#pragma unroll
+  for (int u = 0; u < PK; u++) ld.kload(u, kr[u]);
+  for (int64_t i0 = 0; i0 < nit; i0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t i = i0 + u;
+      ld.kload(i + PK, kr[(u + PK) % (PK + 1)]);
+      ld.vload(i + SV - 1, arr((u + SV - 1) % SV) + wslot);
+      if (i < nit) compute(kr[u % (PK + 1)], u % SV, wave + kWaves * i);
+    }
   }
 
-  if (!colv) return;
-  T* __restrict__ out = static_cast<T*>(p.out) + ((b * p.H + head) * p.qL + srow) * D + dw0;
+  // Merge the 4 chains in order through LDS, one column tile at a time: o of
+  // chain c in va0, (m, l) in va1 (the value slots are free once every
+  // wave's loads and reads have completed).
+  uint4* const mo = va0;
+  float2* const ml = reinterpret_cast<float2*>(va1);
 #pragma unroll
-  for (int db = 0; db < NB; db++) {
-    unsigned short ob[4];
+  for (int ct = 0; ct < CT; ct++) {
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    asm volatile("s_barrier" ::: "memory");
 #pragma unroll
-    for (int e = 0; e < 4; e++) ob[e] = tbits((T)(l == 0.f ? o[db][e] : o[db][e] / l));
-    *reinterpret_cast<uint2*>(out + 16 * db + 4 * g) =
-        make_uint2(ob[0] | ((uint32_t)ob[1] << 16), ob[2] | ((uint32_t)ob[3] << 16));
+    for (int db = 0; db < NB; db++)
+      st16(mo + (wave * NB + db) * 64 + lane, __builtin_bit_cast(uint4, o[ct][db]));
+    ml[wave * 64 + lane] = make_float2(m[ct], l[ct]);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    asm volatile("s_barrier" ::: "memory");
+    float mc[kWaves], lc[kWaves], ec[kWaves];
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int c = 0; c < kWaves; c++) {
+      const float2 v = ml[c * 64 + lane];
+      mc[c] = v.x;
+      lc[c] = v.y;
+      M = fmaxf(M, mc[c]);
+    }
+    float L = 0.f;
+#pragma unroll
+    for (int c = 0; c < kWaves; c++) {
+      ec[c] = __builtin_amdgcn_exp2f(mc[c] - M);
+      L = __builtin_fmaf(lc[c], ec[c], L);
+    }
+    T* __restrict__ out =
+        static_cast<T*>(p.out) + ((b * p.H + head[ct]) * p.qL + srow[ct]) * D + ws * C::DW;
+    // Wave w writes out the dim blocks w, w + 4, ... of this workgroup.
+#pragma unroll
+    for (int k = 0; k < (NB + kWaves - 1) / kWaves; k++) {
+      const int db = wave + kWaves * k;
+      if (db >= NB) break;
+      f32x4_t O = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kWaves; c++) {
+        const f32x4_t oc = __builtin_bit_cast(f32x4_t, ld16(mo + (c * NB + db) * 64 + lane));
+#pragma unroll
+        for (int e = 0; e < 4; e++) O[e] = __builtin_fmaf(oc[e], ec[c], O[e]);
+      }
+      unsigned short ob[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) ob[e] = tbits((T)(L == 0.f ? O[e] : O[e] / L));
+      if (colv[ct])
+        *reinterpret_cast<uint2*>(out + 16 * db + 4 * g) =
+            make_uint2(ob[0] | ((uint32_t)ob[1] << 16), ob[2] | ((uint32_t)ob[3] << 16));
+    }
   }
 }
 
 using Fn = void (*)(SdpaArgs);
 
-// Shapes: "wide" (4 column tiles, each wave all dims) whenever its
-// workgroups fill the GPU or a kv head has more than 16 columns (prefill);
-// "narrow" (1 column tile, dims split over the 4 waves and over workgroups)
-// for small decode batches, where the wide grid would leave compute units
-// idle.
 struct Shape {
   Fn fn;
   int cols, ws;
 };
 
+// Shapes: "rows" (two column tiles per workgroup, one for D = 256) when a kv
+// head has more than 16 columns (prefill); otherwise one column tile, with
+// the dims split over WS workgroups when the decode grid would leave compute
+// units idle. Keys one block ahead and values in two slots: deeper prefetch
+// measured slower (larger unrolled loops, more registers).
 template <typename T, int D>
 Shape shape_for(int64_t ncol, int64_t streams, int cus) {
-  constexpr int NDB = D / 16;
-  const int64_t wide_wgs = streams * ((ncol + 63) / 64);
-  if (ncol > 16 || wide_wgs >= cus) return {sdpa_mfma_kernel<T, D, 4, NDB>, 64, 1};
-  using N = Attn<T, D, 1, 1>;
-  return {sdpa_mfma_kernel<T, D, 1, 1>, 16, N::WS};
+  constexpr int CT_ROWS = D == 256 ? 1 : 2;
+  constexpr int PK = D == 256 ? 0 : 1;
+  constexpr int WS8 = D / 16 < 8 ? D / 16 : 8;  // at least two value chunks per row
+  if (ncol > 16) return {sdpa_mfma_kernel<T, D, CT_ROWS, PK, 2, 1>, 16 * CT_ROWS, 1};
+  if (streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 1>, 16, 1};
+  if (2 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 2>, 16, 2};
+  if (4 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 4>, 16, 4};
+  return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS8>, 16, WS8};
 }
 
 template <typename T>
