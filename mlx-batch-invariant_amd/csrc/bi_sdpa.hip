@@ -43,6 +43,7 @@
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int64_t kMaskSlack = 64;  // keys a block may read past N
 constexpr int kPartials = 32;
 constexpr int kGroupLanes = 8;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -422,13 +423,16 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
   p.mask_mode = mask_mode;
   p.causal_offset = mask_mode == BI_MASK_CAUSAL ? causal_offset : 0;
 
-  // The MFMA kernel addresses 32 key / value rows from a block's first row
-  // with 32-bit byte offsets.
+  // The MFMA kernel addresses 32 key / value rows from a block's first row,
+  // and a batch's mask, with 32-bit byte offsets.
   if (dtype != BI_F32) {
     const int64_t st = p.ks[2] > p.vs[2] ? p.ks[2] : p.vs[2];
     if ((32 * st + D) * esz > INT32_MAX)
       return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: key/value row stride %lld is too large",
                       (long long)st);
+    if (mask_mode == BI_MASK_ARRAY &&
+        ((H - 1) * p.ms[1] + (qL - 1) * p.ms[2] + N + kMaskSlack) * esz > INT32_MAX)
+      return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: the mask of one batch entry is too large");
   }
   // fp32 runs on the VALU kernel above; bf16 and f16 on matrix cores
   // (bi_sdpa_mfma.hip). Each is the only arithmetic for its element type.

@@ -162,16 +162,17 @@ __device__ inline float col_max(float x) { return half_pair(row_pair(x, true), t
 // Launch shape: CT column tiles of 16 columns per workgroup, shared by the 4
 // waves (one chain each); WS workgroups split a column tile's output dims
 // (each computes the same scores and statistics, and o for D / WS dims); a
-// wave's keys are loaded PK blocks ahead into the score MFMAs' registers and
-// its values SV - 1 blocks ahead into its own LDS slots. None of these
-// enters a column's arithmetic.
-template <typename T, int D, int CT, int PK, int SV, int WS>
+// wave's keys are loaded PK blocks ahead into registers and its values
+// SV - 1 blocks ahead into its own LDS slots; an array mask's values (MK) are
+// loaded with the keys (MK = 1) or at the start of their own block (MK = 2,
+// one register set). None of these enters a column's arithmetic.
+template <typename T, int D, int CT, int PK, int SV, int WS, int MK>
 struct Chain {
   static constexpr int NQ = D / 32;            // score MFMAs per 16 keys
   static constexpr int DW = D / WS;            // output dims per workgroup
   static constexpr int NB = DW / 16;           // 16-dim blocks of o held
   static constexpr int VCH = DW / 8;           // 16-byte chunks per value row held
-  static constexpr int NKL = 2 * NQ;           // key loads per block per lane
+  static constexpr int NKL = 2 * NQ + (MK ? 8 * CT : 0);  // key and mask loads per block
   static constexpr int DV = kBlk * VCH / 64;   // value LDS-DMA loads per block
   static constexpr int VSLOT = kBlk * VCH;     // uint4 per value slot
   static constexpr int ARR_U4 = kWaves * VSLOT;  // one slot of every wave
@@ -198,18 +199,26 @@ struct Chain {
     return ((((r & 3) << 1) | (((r >> 3) & 1) << 3))) & (VCH - 1);
   }
 
-  // Key and value rows of the stream. Each block's buffer resources start at
-  // the block's first row, so the lane offsets are the same for every block
-  // (and below 2^31: the host bounds 32 * stride); loads for blocks i >= nit
-  // use an empty resource, which reads nothing and returns zeros.
+  // Key and value rows of the stream, and the batch's mask. Each block's
+  // buffer resources start at the block's first row (first key for the mask),
+  // so the lane offsets are the same for every block (and below 2^31: the
+  // host bounds 32 * stride and the mask's extent); loads for blocks
+  // i >= nit use an empty resource, which reads nothing and returns zeros.
   const T* kb;
   const T* vb;
-  int64_t ks2, vs2, N, nit;
+  const T* mb;
+  int64_t ks2, vs2, N, nit, mext;
   int wave;
-  uint32_t koff[2][NQ], voff[DV];
+  // Lane byte offsets: key row 16kt + r16 at dims 8g ..; value chunk j;
+  // mask keys 4g .. of the lane's row in each column tile. The other key and
+  // mask loads add constants (immediate offsets, which the range check
+  // includes; a scalar offset would not be checked).
+  uint32_t koff[2], voff[DV], moff[MK ? CT : 1];
 
+  // mrow: this lane's mask row offset (elements from the batch's mask) per
+  // column tile.
   __device__ __forceinline__ void init(const SdpaArgs& p, int64_t b, int64_t kvh, int ws, int w,
-                                       int64_t n_it, int lane) {
+                                       int64_t n_it, int lane, const int64_t* mrow) {
     constexpr uint32_t E = sizeof(T);
     const int g = lane >> 4, r16 = lane & 15;
     kb = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
@@ -219,11 +228,15 @@ struct Chain {
     N = p.N;
     nit = n_it;
     wave = w;
+    if constexpr (MK) {
+      // Elements of the batch's mask that any (head, row) reaches.
+      mb = static_cast<const T*>(p.mask) + b * p.ms[0];
+      mext = (p.H - 1) * p.ms[1] + (p.qL - 1) * p.ms[2] + N;
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+      for (int ct = 0; ct < CT; ct++) moff[ct] = (uint32_t)((mrow[ct] + 4 * g) * E);
+    }
 #pragma unroll
-      for (int i = 0; i < NQ; i++)
-        koff[kt][i] = (uint32_t)(((16 * kt + r16) * ks2 + 32 * i + 8 * g) * E);
+    for (int kt = 0; kt < 2; kt++) koff[kt] = (uint32_t)(((16 * kt + r16) * ks2 + 8 * g) * E);
 #pragma unroll
     for (int j = 0; j < DV; j++) {
       const int pos = j * 64 + lane, r = pos / VCH, c = (pos % VCH) ^ swz_v(r);
@@ -238,15 +251,36 @@ struct Chain {
                      in ? ((N - key0 - 1) * stride + D) * (int64_t)sizeof(T) : 0);
   }
   // Keys of block i into the score MFMAs' A operands: lane (r16, g) holds
-  // K[16kt + r16][32q + 8g .. + 7].
-  __device__ __forceinline__ void kload(int64_t i, uint4 (&kr)[2][NQ]) const {
+  // K[16kt + r16][32q + 8g .. + 7]. Mask values: those of the lane's keys
+  // 16kt + 4g + e (j = 4kt + e) in each column tile.
+  struct KRegs {
+    uint4 k[2][NQ];
+    unsigned short m[MK == 1 ? CT : 1][8];
+  };
+  struct MRegs {
+    unsigned short m[CT][8];
+  };
+  __device__ __forceinline__ void mload(int64_t i, unsigned short (&m)[CT][8]) const {
+    const int64_t key0 = (wave + kWaves * i) * kBlk;
+    const bool in = i < nit;
+    const auto rm = make_rsrc(mb + (in ? key0 : 0), in ? (mext - key0) * (int64_t)sizeof(T) : 0);
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        m[ct][j] = __builtin_amdgcn_raw_buffer_load_b16(
+            rm, (int)(moff[ct] + (16 * (j >> 2) + (j & 3)) * sizeof(T)), 0, 0);
+  }
+  __device__ __forceinline__ void kload(int64_t i, KRegs& kr) const {
     const auto rs = rsrc(kb, ks2, i);
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
       for (int q = 0; q < NQ; q++)
-        kr[kt][q] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)koff[kt][q], 0, 0));
+        kr.k[kt][q] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(koff[kt] + 32 * q * sizeof(T)),
+                                                         0, 0));
+    if constexpr (MK == 1) mload(i, kr.m);
   }
   // Values of block i into an LDS slot (loads that write LDS directly).
   __device__ __forceinline__ void vload(int64_t i, uint4* dst) const {
@@ -260,9 +294,9 @@ struct Chain {
   }
 };
 
-template <typename T, int D, int CT, int PK, int SV, int WS>
+template <typename T, int D, int CT, int PK, int SV, int WS, int MK>
 __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
-  using C = Chain<T, D, CT, PK, SV, WS>;
+  using C = Chain<T, D, CT, PK, SV, WS, MK>;
   constexpr int NQ = C::NQ, NB = C::NB, VCH = C::VCH;
   constexpr int COLS = 16 * CT;  // columns per workgroup
   // Value slot s of every wave is array s: an LDS read then names the one
@@ -302,8 +336,6 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   };
   const int64_t last_cc = (c0 + COLS < ncol ? c0 + COLS : ncol) - 1;
   const int64_t nblk = (kend_of(last_cc / G) + kBlk - 1) / kBlk;
-  const int nkeys = (int)p.N;
-  const bool has_mask = p.mask_mode == BI_MASK_ARRAY;
 
   // This lane's column in each tile; its query as the B operand of the score
   // MFMAs (Q[col][32i + 8g ..]); its chain state.
@@ -311,7 +343,7 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   int64_t srow[CT], head[CT];
   int kend[CT];
   uint4 qt[CT][NQ];
-  const T* mrow[CT];
+  int64_t mrow[CT];
   float m[CT], l[CT];
   f32x4_t o[CT][NB];
 #pragma unroll
@@ -325,9 +357,7 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
 #pragma unroll
     for (int i = 0; i < NQ; i++)
       qt[ct][i] = colv[ct] ? ld16(qrow + 32 * i + 8 * g) : make_uint4(0, 0, 0, 0);
-    mrow[ct] = has_mask ? static_cast<const T*>(p.mask) + b * p.ms[0] + head[ct] * p.ms[1] +
-                              srow[ct] * p.ms[2]
-                        : nullptr;
+    mrow[ct] = head[ct] * p.ms[1] + srow[ct] * p.ms[2];
     m[ct] = -FLT_MAX;
     l[ct] = 0.f;
     if (wave == 0 && p.sinks && colv[ct]) {
@@ -345,9 +375,11 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   const int64_t nit = nblk > wave ? (nblk - wave + kWaves - 1) / kWaves : 0;
   const int wslot = wave * C::VSLOT;  // this wave's slot within each array
   C ld;
-  ld.init(p, b, kvh, ws, wave, nit, lane);
+  ld.init(p, b, kvh, ws, wave, nit, lane, mrow);
   // One block of this chain: keys in kr, values in value slot `slot`.
-  auto compute = [&](const uint4 (&kr)[2][NQ], int slot, int64_t blk) __attribute__((always_inline)) {
+  constexpr int MKCT = MK ? CT : 1;
+  auto compute = [&](const typename C::KRegs& kr, const unsigned short (&mk)[MKCT][8], int slot,
+                     int64_t blk) __attribute__((always_inline)) {
     // Scores: S^T tiles (16 keys x 16 columns); lane (g, r16) holds keys
     // 16kt + 4g + e of column r16.
     f32x4_t sc[CT][2];
@@ -357,7 +389,7 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
       for (int kt = 0; kt < 2; kt++) {
         sc[ct][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < NQ; i++) sc[ct][kt] = mma32(T(0), kr[kt][i], qt[ct][i], sc[ct][kt]);
+        for (int i = 0; i < NQ; i++) sc[ct][kt] = mma32(T(0), kr.k[kt][i], qt[ct][i], sc[ct][kt]);
       }
     // Key indices fit in 32 bits (the host checks N < 2^31).
     const int key0 = (int)blk * kBlk + 4 * g;
@@ -374,13 +406,12 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
           s[kt][e] = sc[ct][kt][e] * p.scale2;
           use[kt][e] = key0 + 16 * kt + e < kend[ct];
         }
-      if (has_mask) {  // wave-uniform; every lane loads (in bounds), unused lanes ignore it
+      if constexpr (MK) {  // keys past N read 0 and are unused
 #pragma unroll
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            const int key = key0 + 16 * kt + e;
-            const float mv = (float)mrow[ct][key < nkeys ? key : 0];
+            const float mv = (float)__builtin_bit_cast(T, mk[ct][4 * kt + e]);
             use[kt][e] = use[kt][e] && mv > -3.0e38f;
             s[kt][e] = s[kt][e] + mv * kLog2e;
           }
@@ -480,7 +511,8 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   // least common multiple of the two rotations) so that register and slot
   // indices are compile-time.
   constexpr int U = lcm(PK + 1, SV);
-  uint4 kr[PK + 1][2][NQ];
+  typename C::KRegs kr[PK + 1];
+  typename C::MRegs mcur;  // MK == 2: this step's mask values
 #pragma unroll
   for (int u = 0; u < SV - 1; u++) ld.vload(u, arr(u) + wslot);
 #pragma unroll
@@ -489,9 +521,15 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int64_t i = i0 + u;
+      if constexpr (MK == 2) ld.mload(i, mcur.m);
       ld.kload(i + PK, kr[(u + PK) % (PK + 1)]);
       ld.vload(i + SV - 1, arr((u + SV - 1) % SV) + wslot);
-      if (i < nit) compute(kr[u % (PK + 1)], u % SV, wave + kWaves * i);
+      if (i < nit) {
+        if constexpr (MK == 2)
+          compute(kr[u % (PK + 1)], mcur.m, u % SV, wave + kWaves * i);
+        else
+          compute(kr[u % (PK + 1)], kr[u % (PK + 1)].m, u % SV, wave + kWaves * i);
+      }
     }
   }
 
@@ -556,29 +594,37 @@ struct Shape {
   int cols, ws;
 };
 
-// Shapes: "rows" (two column tiles per workgroup, one for D = 256) when a kv
-// head has more than 16 columns (prefill); otherwise one column tile, with
-// the dims split over WS workgroups when the decode grid would leave compute
-// units idle. Keys one block ahead and values in two slots: deeper prefetch
-// measured slower (larger unrolled loops, more registers).
-template <typename T, int D>
+// Shapes: "rows" (two column tiles per workgroup, one for D = 256; mask
+// values loaded in their own block, for registers) when a kv head has more
+// than 16 columns (prefill); otherwise one column tile, with the dims split
+// over WS workgroups when the decode grid would leave compute units idle (and
+// always at least in two for D = 256). Keys one
+// block ahead and values in two slots: deeper prefetch measured no faster.
+template <typename T, int D, bool MASK>
 Shape shape_for(int64_t ncol, int64_t streams, int cus) {
   constexpr int CT_ROWS = D == 256 ? 1 : 2;
+  constexpr int MK = MASK ? 1 : 0, MK_ROWS = MASK ? 2 : 0;
   constexpr int PK = D == 256 ? 0 : 1;
+  constexpr int WS1 = D == 256 ? 2 : 1;  // D = 256 always splits: registers
   constexpr int WS8 = D / 16 < 8 ? D / 16 : 8;  // at least two value chunks per row
-  if (ncol > 16) return {sdpa_mfma_kernel<T, D, CT_ROWS, PK, 2, 1>, 16 * CT_ROWS, 1};
-  if (streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 1>, 16, 1};
-  if (2 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 2>, 16, 2};
-  if (4 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 4>, 16, 4};
-  return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS8>, 16, WS8};
+  if (ncol > 16) return {sdpa_mfma_kernel<T, D, CT_ROWS, PK, 2, WS1, MK_ROWS>, 16 * CT_ROWS, WS1};
+  if (streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS1, MK>, 16, WS1};
+  if (2 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 2, MK>, 16, 2};
+  if (4 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 4, MK>, 16, 4};
+  return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS8, MK>, 16, WS8};
+}
+
+template <typename T, int D>
+Shape shape_for_mask(bool mask, int64_t ncol, int64_t streams, int cus) {
+  return mask ? shape_for<T, D, true>(ncol, streams, cus) : shape_for<T, D, false>(ncol, streams, cus);
 }
 
 template <typename T>
-Shape shape_for_dims(int64_t D, int64_t ncol, int64_t streams, int cus) {
+Shape shape_for_dims(int64_t D, bool mask, int64_t ncol, int64_t streams, int cus) {
   switch (D) {
-    case 64: return shape_for<T, 64>(ncol, streams, cus);
-    case 128: return shape_for<T, 128>(ncol, streams, cus);
-    case 256: return shape_for<T, 256>(ncol, streams, cus);
+    case 64: return shape_for_mask<T, 64>(mask, ncol, streams, cus);
+    case 128: return shape_for_mask<T, 128>(mask, ncol, streams, cus);
+    case 256: return shape_for_mask<T, 256>(mask, ncol, streams, cus);
   }
   return {nullptr, 0, 0};
 }
@@ -588,8 +634,9 @@ Shape shape_for_dims(int64_t D, int64_t ncol, int64_t streams, int cus) {
 bool sdpa_mfma_launch(const SdpaArgs& p, int dtype, int64_t D, int cus, hipStream_t stream) {
   const int64_t ncol = (p.H / p.Hkv) * p.qL;
   const int64_t streams = p.B * p.Hkv;
-  const Shape sh = dtype == BI_BF16 ? shape_for_dims<__bf16>(D, ncol, streams, cus)
-                 : dtype == BI_F16  ? shape_for_dims<_Float16>(D, ncol, streams, cus)
+  const bool mask = p.mask_mode == BI_MASK_ARRAY;
+  const Shape sh = dtype == BI_BF16 ? shape_for_dims<__bf16>(D, mask, ncol, streams, cus)
+                 : dtype == BI_F16  ? shape_for_dims<_Float16>(D, mask, ncol, streams, cus)
                                     : Shape{nullptr, 0, 0};
   if (!sh.fn) return false;
   const int64_t ncb = (ncol + sh.cols - 1) / sh.cols;

@@ -118,6 +118,33 @@ def test_causal_and_masks_are_invariant(cuda):
                     assert int((got != base).sum()) == 0, "sdpa %s %s qL=%d" % (label, dname, qL)
 
 
+def test_masked_decode_is_batch_invariant(cuda):
+    """An additive and a boolean mask per batch entry: a sequence's row has the
+    same bits alone and at batch sizes whose grids take every launch shape
+    (dims split over 8, 4, 2 workgroups and unsplit)."""
+    H, Hkv, N, D = 32, 8, 1000, 128
+    g = torch.Generator().manual_seed(36)
+    for dname, dtype in DTYPES:
+        if dtype == torch.float32:
+            continue
+        q1, k1, v1 = (rn((1, H, 1, D), dtype, 37, device=cuda), rn((1, Hkv, N, D), dtype, 38, device=cuda),
+                      rn((1, Hkv, N, D), dtype, 39, device=cuda))
+        qp, kp, vp = (rn((64, H, 1, D), dtype, 40, device=cuda), rn((64, Hkv, N, D), dtype, 41, device=cuda),
+                      rn((64, Hkv, N, D), dtype, 42, device=cuda))
+        add = rn((64, 1, 1, N), dtype, 43, device=cuda)
+        add[:, :, :, ::5] = -float("inf")
+        keep = (torch.rand(64, 1, 1, N, generator=g) > 0.2).to(cuda)
+        for label, mpool in (("additive", add), ("bool", keep)):
+            m1 = mpool[7:8]
+            base = bits(bi.scaled_dot_product_attention(q1, k1, v1, mask=m1)[0])
+            for B in (2, 5, 17, 40, 64):
+                idx = B // 2
+                mb = torch.cat([mpool[:idx], m1, mpool[idx + 1:B]]) if B > 1 else m1
+                y = bi.scaled_dot_product_attention(batch_with(q1, qp, B, idx), batch_with(k1, kp, B, idx),
+                                                    batch_with(v1, vp, B, idx), mask=mb)
+                assert int((bits(y[idx]) != base).sum()) == 0, "%s %s B=%d" % (label, dname, B)
+
+
 def test_context_growth_chunked_prefill(cuda):
     """32/8 heads, D=128, bf16; KV grown 4000 -> 4200 with the
     new keys masked. A query row's result computed over the first N' keys must
