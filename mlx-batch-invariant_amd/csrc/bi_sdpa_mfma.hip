@@ -118,6 +118,12 @@ __device__ __forceinline__ u32x2_t ds_read_tr(uint32_t lds_addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(lds_addr) : "memory");
   return v;
 }
+// A 16-byte LDS read as an asm statement, for the same reason.
+__device__ __forceinline__ u32x4_t ds_read_b128(uint32_t lds_addr) {
+  u32x4_t v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_addr) : "memory");
+  return v;
+}
 
 template <typename T> __device__ inline unsigned short tbits(T x) {
   return __builtin_bit_cast(unsigned short, x);
@@ -162,35 +168,42 @@ __device__ inline float col_max(float x) { return half_pair(row_pair(x, true), t
 // Launch shape: CT column tiles of 16 columns per workgroup, shared by the 4
 // waves (one chain each); WS workgroups split a column tile's output dims
 // (each computes the same scores and statistics, and o for D / WS dims); a
-// wave's keys are loaded PK blocks ahead into registers and its values
-// SV - 1 blocks ahead into its own LDS slots; an array mask's values (MK) are
+// wave's keys are loaded PK blocks ahead into registers (or, KL, into its
+// LDS slots beside the values, by contiguous loads) and its values SV - 1
+// blocks ahead into its own LDS slots; an array mask's values (MK) are
 // loaded with the keys (MK = 1) or at the start of their own block (MK = 2,
 // one register set). None of these enters a column's arithmetic.
-template <typename T, int D, int CT, int PK, int SV, int WS, int MK>
+template <typename T, int D, int CT, int PK, int SV, int WS, int MK, bool KL>
 struct Chain {
   static constexpr int NQ = D / 32;            // score MFMAs per 16 keys
   static constexpr int DW = D / WS;            // output dims per workgroup
   static constexpr int NB = DW / 16;           // 16-dim blocks of o held
   static constexpr int VCH = DW / 8;           // 16-byte chunks per value row held
-  static constexpr int NKL = 2 * NQ + (MK ? 8 * CT : 0);  // key and mask loads per block
+  static constexpr int CH = D / 8;             // 16-byte chunks per key row
+  static constexpr int NKL = (KL ? 0 : 2 * NQ) + (MK ? 8 * CT : 0);  // register loads per block
+  static constexpr int DK = KL ? kBlk * CH / 64 : 0;  // key LDS-DMA loads per block
   static constexpr int DV = kBlk * VCH / 64;   // value LDS-DMA loads per block
-  static constexpr int VSLOT = kBlk * VCH;     // uint4 per value slot
+  static constexpr int KSLOT = KL ? kBlk * CH : 0;  // uint4 of keys per slot
+  static constexpr int VSLOT = KSLOT + kBlk * VCH;  // uint4 per slot (keys, then values)
   static constexpr int ARR_U4 = kWaves * VSLOT;  // one slot of every wave
-  // Value reads as asm statements (see ds_read_tr) except with 8 value loads
-  // per block, where the compiler's own waits before the intrinsic read were
-  // checked to be exactly VWAIT and it schedules the products among the reads.
-  static constexpr bool ASM_TR = DV != 8;
+  // LDS reads as asm statements (see ds_read_tr) except with 8 value loads
+  // per block and keys in registers, where the compiler's own waits before
+  // the intrinsic read were checked to be exactly VWAIT and it schedules the
+  // products among the reads.
+  static constexpr bool ASM_TR = KL || DV != 8;
   // Vector-memory operations issued after a block's value loads and before
   // its values are read: at least those of the SV - 1 blocks issued since
   // (the prologue issues the first SV - 1 value blocks before the first PK
   // key blocks, which keeps the count when PK >= SV - 2).
-  static constexpr int VWAIT = (SV - 1) * (NKL + DV);
-  static_assert(SV >= 2 && SV <= 6 && PK >= 0 && PK >= SV - 2 && D % (16 * WS) == 0 && VCH >= 2,
+  static constexpr int VWAIT = (SV - 1) * (NKL + DK + DV);
+  static_assert(SV >= 2 && SV <= 6 && PK >= 0 && (KL ? PK == 0 && !MK : PK >= SV - 2) &&
+                    D % (16 * WS) == 0 && VCH >= 2,
                 "shape");
   static_assert(VWAIT <= 63, "value loads in flight exceed the vmcnt range");
+  static_assert(SV * ARR_U4 * 16 <= 160 * 1024, "LDS per workgroup");
   // The merge stages one column tile at a time: every chain's o fills one
   // slot array exactly and its (m, l) fit in another.
-  static_assert(kWaves * NB * 64 == ARR_U4 && kWaves * 64 / 2 <= ARR_U4, "merge staging");
+  static_assert(kWaves * NB * 64 <= ARR_U4 && kWaves * 64 / 2 <= ARR_U4, "merge staging");
 
   // Value slot: [32 keys][VCH chunks], chunk c of key r at c ^ swz_v(r):
   // ds_read_tr16_b64 reads four consecutive keys of 16 dims, and the swizzle
@@ -198,6 +211,9 @@ struct Chain {
   __device__ __forceinline__ static int swz_v(int r) {
     return ((((r & 3) << 1) | (((r >> 3) & 1) << 3))) & (VCH - 1);
   }
+  // Key slot (KL): [32 keys][CH chunks], chunk c of key r at c ^ swz_k(r): the
+  // score MFMAs' A reads (16 keys, one chunk each) then hit distinct banks.
+  __device__ __forceinline__ static int swz_k(int r) { return r & ((CH < 16 ? CH : 16) - 1); }
 
   // Key and value rows of the stream, and the batch's mask. Each block's
   // buffer resources start at the block's first row (first key for the mask),
@@ -213,7 +229,7 @@ struct Chain {
   // mask keys 4g .. of the lane's row in each column tile. The other key and
   // mask loads add constants (immediate offsets, which the range check
   // includes; a scalar offset would not be checked).
-  uint32_t koff[2], voff[DV], moff[MK ? CT : 1];
+  uint32_t koff[2], kdoff[KL ? DK : 1], voff[DV], moff[MK ? CT : 1];
 
   // mrow: this lane's mask row offset (elements from the batch's mask) per
   // column tile.
@@ -241,6 +257,13 @@ struct Chain {
     for (int j = 0; j < DV; j++) {
       const int pos = j * 64 + lane, r = pos / VCH, c = (pos % VCH) ^ swz_v(r);
       voff[j] = (uint32_t)((r * vs2 + ws * DW + c * 8) * E);
+    }
+    if constexpr (KL) {
+#pragma unroll
+      for (int j = 0; j < DK; j++) {
+        const int pos = j * 64 + lane, r = pos / CH, c = (pos % CH) ^ swz_k(r);
+        kdoff[j] = (uint32_t)((r * ks2 + c * 8) * E);
+      }
     }
   }
   __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const T* base, int64_t stride,
@@ -272,31 +295,41 @@ struct Chain {
             rm, (int)(moff[ct] + (16 * (j >> 2) + (j & 3)) * sizeof(T)), 0, 0);
   }
   __device__ __forceinline__ void kload(int64_t i, KRegs& kr) const {
-    const auto rs = rsrc(kb, ks2, i);
+    if constexpr (!KL) {
+      const auto rs = rsrc(kb, ks2, i);
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+      for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int q = 0; q < NQ; q++)
-        kr.k[kt][q] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(koff[kt] + 32 * q * sizeof(T)),
-                                                         0, 0));
+        for (int q = 0; q < NQ; q++)
+          kr.k[kt][q] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(koff[kt] + 32 * q * sizeof(T)),
+                                                           0, 0));
+    }
     if constexpr (MK == 1) mload(i, kr.m);
   }
-  // Values of block i into an LDS slot (loads that write LDS directly).
+  // Keys (KL) and values of block i into an LDS slot (loads that write LDS
+  // directly; the keys of a slot first, then its values).
   __device__ __forceinline__ void vload(int64_t i, uint4* dst) const {
-    const auto rs = rsrc(vb, vs2, i);
-    // The slot's previous reads have returned before new values land.
+    // The slot's previous reads have returned before new data lands.
     __builtin_amdgcn_s_waitcnt(kWaitLds);
+    if constexpr (KL) {
+      const auto rk = rsrc(kb, ks2, i);
+#pragma unroll
+      for (int j = 0; j < DK; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(dst + j * 64), 16,
+                                                 (int)kdoff[j], 0, 0, 0);
+    }
+    const auto rs = rsrc(vb, vs2, i);
 #pragma unroll
     for (int j = 0; j < DV; j++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + j * 64), 16, (int)voff[j],
-                                               0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + KSLOT + j * 64), 16,
+                                               (int)voff[j], 0, 0, 0);
   }
 };
 
-template <typename T, int D, int CT, int PK, int SV, int WS, int MK>
+template <typename T, int D, int CT, int PK, int SV, int WS, int MK, bool KL>
 __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
-  using C = Chain<T, D, CT, PK, SV, WS, MK>;
+  using C = Chain<T, D, CT, PK, SV, WS, MK, KL>;
   constexpr int NQ = C::NQ, NB = C::NB, VCH = C::VCH;
   constexpr int COLS = 16 * CT;  // columns per workgroup
   // Value slot s of every wave is array s: an LDS read then names the one
@@ -380,6 +413,26 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   constexpr int MKCT = MK ? CT : 1;
   auto compute = [&](const typename C::KRegs& kr, const unsigned short (&mk)[MKCT][8], int slot,
                      int64_t blk) __attribute__((always_inline)) {
+    // Keys from the slot (KL): the slot's loads have landed (at most VWAIT
+    // younger operations in flight), then lane (r16, g) reads chunk 4q + g of
+    // key 16kt + r16.
+    u32x4_t kl[KL ? 2 : 1][KL ? NQ : 1];
+    if constexpr (KL) {
+      __builtin_amdgcn_s_waitcnt(wait_vm(C::VWAIT));
+      const uint32_t ks = (uint32_t)(uintptr_t)(lds_void_t*)(arr(slot) + wslot);
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+          const int r = 16 * kt + r16;
+          kl[kt][i] = ds_read_b128(ks + (r * C::CH + ((4 * i + g) ^ C::swz_k(r))) * 16);
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int i = 0; i < NQ; i++) asm volatile("" : "+v"(kl[kt][i]));
+    }
     // Scores: S^T tiles (16 keys x 16 columns); lane (g, r16) holds keys
     // 16kt + 4g + e of column r16.
     f32x4_t sc[CT][2];
@@ -389,7 +442,10 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
       for (int kt = 0; kt < 2; kt++) {
         sc[ct][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < NQ; i++) sc[ct][kt] = mma32(T(0), kr.k[kt][i], qt[ct][i], sc[ct][kt]);
+        for (int i = 0; i < NQ; i++) {
+          const uint4 a = KL ? __builtin_bit_cast(uint4, kl[KL ? kt : 0][KL ? i : 0]) : kr.k[kt][i];
+          sc[ct][kt] = mma32(T(0), a, qt[ct][i], sc[ct][kt]);
+        }
       }
     // Key indices fit in 32 bits (the host checks N < 2^31).
     const int key0 = (int)blk * kBlk + 4 * g;
@@ -462,9 +518,9 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
       }
     // The block's values have landed in the slot (vector memory completes in
     // order: at most VWAIT younger operations may still be in flight).
-    __builtin_amdgcn_s_waitcnt(wait_vm(C::VWAIT));
+    if constexpr (!KL) __builtin_amdgcn_s_waitcnt(wait_vm(C::VWAIT));
     asm volatile("" ::: "memory");
-    uint4* const vslot = arr(slot) + wslot;
+    uint4* const vslot = arr(slot) + wslot + C::KSLOT;
     u32x2_t va[NB][2];
 #pragma unroll
     for (int db = 0; db < NB; db++) {
@@ -607,11 +663,16 @@ Shape shape_for(int64_t ncol, int64_t streams, int cus) {
   constexpr int PK = D == 256 ? 0 : 1;
   constexpr int WS1 = D == 256 ? 2 : 1;  // D = 256 always splits: registers
   constexpr int WS8 = D / 16 < 8 ? D / 16 : 8;  // at least two value chunks per row
-  if (ncol > 16) return {sdpa_mfma_kernel<T, D, CT_ROWS, PK, 2, WS1, MK_ROWS>, 16 * CT_ROWS, WS1};
-  if (streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS1, MK>, 16, WS1};
-  if (2 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 2, MK>, 16, 2};
-  if (4 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, 4, MK>, 16, 4};
-  return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS8, MK>, 16, WS8};
+  // Split decode without a mask: keys through LDS by contiguous loads (three
+  // slots); with a mask or D != 128, keys in registers
+  // (measured faster for D = 128 only; D = 256 key slots would not fit LDS).
+  constexpr bool KLS = !MASK && D == 128;
+  constexpr int PKS_ = KLS ? 0 : PK, SVS_ = KLS ? 3 : 2;
+  if (ncol > 16) return {sdpa_mfma_kernel<T, D, CT_ROWS, PK, 2, WS1, MK_ROWS, false>, 16 * CT_ROWS, WS1};
+  if (streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS1, MK, false>, 16, WS1};
+  if (2 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 2, MK, KLS>, 16, 2};
+  if (4 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 4, MK, KLS>, 16, 4};
+  return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, WS8, MK, KLS>, 16, WS8};
 }
 
 template <typename T, int D>
