@@ -95,11 +95,18 @@ int bi_gemm(const void* a, const void* b, const void* bias, void* out,
  *   scale multiplies q.k; H must be a multiple of Hkv (GQA: head h reads
  *         kv head h / (H / Hkv))
  *
- * Key i is owned by partial (i mod 32) and walked in ascending order; the 32
- * partials are combined in a fixed order. Nothing in the reduction depends on
+ * One fixed reduction per element type. BI_F32: key i is owned by partial
+ * (i mod 32) and walked in ascending order; the 32 partials are combined in a
+ * fixed order. BI_F16 / BI_BF16 (matrix cores): keys are taken in blocks of
+ * 32, block b owned by chain (b mod 4) and walked in ascending order; the 4
+ * chains are combined in a fixed order. Nothing in the reduction depends on
  * B, qL, the other query rows, or N beyond which keys exist, so growing the
  * context with masked keys leaves earlier results bitwise unchanged. A query
- * row whose keys are all masked yields 0.
+ * row whose keys are all masked yields 0. Values of keys that an array mask
+ * hides from every query sharing a workgroup are never used, whatever they
+ * hold (as in the reference, which skips masked keys); the matrix-core path
+ * multiplies the values of other unused keys in a block (another query's
+ * masked or future keys) by zero, so those must be finite.
  * Supported head dims: D == V in {64, 128, 256}.
  */
 int bi_sdpa(const void* q, const void* k, const void* v,

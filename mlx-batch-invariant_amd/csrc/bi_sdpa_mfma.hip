@@ -451,6 +451,7 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
     const int key0 = (int)blk * kBlk + 4 * g;
     uint2 ph[CT][2], pl[CT][2];
     float f[CT];
+    uint32_t used = 0;  // mask: bit 4kt + e set if this lane's column uses key 16kt + 4g + e
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) {
       float s[2][4];
@@ -476,7 +477,10 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
+        for (int e = 0; e < 4; e++) {
+          bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
+          if constexpr (MK != 0) used |= use[kt][e] ? 1u << (4 * kt + e) : 0u;
+        }
       bm = col_max(bm);
       const bool any = bm > -INFINITY;
       const float mn = any ? fmaxf(m[ct], bm) : m[ct];
@@ -547,6 +551,34 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
       for (int db = 0; db < NB; db++) asm volatile("" : "+v"(va[db][0]), "+v"(va[db][1]));
+    }
+    // With an array mask, values of keys that no column of the workgroup uses
+    // are zeroed, as the reference never reads them (they may hold anything,
+    // e.g. an unwritten cache slot behind a padding mask). Their p is +0 in
+    // every column and o is never -0.0, so for finite values this changes no
+    // bit. Lane group g holds keys 16kt + 4g + t, t = 0..3; the ballots' 16-bit
+    // field g covers their columns. (Without a mask the only keys no column
+    // uses are past N, which load as zeros, or keys past a start-aligned causal
+    // bound, which hold real data.)
+    // OR over the 16 columns of the lane's row group (rotations by 1, 2, 4, 8
+    // within each row of 16 lanes): bit 4kt + t set if some column uses key
+    // 16kt + 4g + t.
+    if constexpr (MK != 0) {
+      used |= __builtin_amdgcn_mov_dpp((int)used, 0x121, 0xF, 0xF, false);  // row_ror:1
+      used |= __builtin_amdgcn_mov_dpp((int)used, 0x122, 0xF, 0xF, false);  // row_ror:2
+      used |= __builtin_amdgcn_mov_dpp((int)used, 0x124, 0xF, 0xF, false);  // row_ror:4
+      used |= __builtin_amdgcn_mov_dpp((int)used, 0x128, 0xF, 0xF, false);  // row_ror:8
+    }
+    if (MK != 0 && __builtin_amdgcn_ballot_w64(used != 0xFFu) != 0) {  // wave-uniform
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        uint32_t keep[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) keep[t] = (used >> (4 * kt + t)) & 1 ? 0xFFFFu : 0u;
+        const u32x2_t vm = {keep[0] | (keep[1] << 16), keep[2] | (keep[3] << 16)};
+#pragma unroll
+        for (int db = 0; db < NB; db++) va[db][kt] &= vm;
+      }
     }
 #pragma unroll
     for (int db = 0; db < NB; db++) {

@@ -145,6 +145,31 @@ def test_masked_decode_is_batch_invariant(cuda):
                 assert int((bits(y[idx]) != base).sum()) == 0, "%s %s B=%d" % (label, dname, B)
 
 
+def test_values_behind_a_mask_are_never_read(cuda):
+    """The reference skips masked keys (_attention.py:94-96), so whatever their
+    value rows hold (here NaN, as in an unwritten cache slot behind a padding
+    mask) cannot reach the output: bitwise equal to the same call with those
+    rows zeroed, for decode and prefill shapes."""
+    H, Hkv, N, D = 8, 2, 300, 128
+    for dname, dtype in DTYPES:
+        for B, qL in ((3, 1), (1, 40)):
+            q = rn((B, H, qL, D), dtype, 44, device=cuda)
+            k = rn((B, Hkv, N, D), dtype, 45, device=cuda)
+            v = rn((B, Hkv, N, D), dtype, 46, device=cuda)
+            keep = torch.ones(B, 1, 1, N, dtype=torch.bool)
+            keep[..., 250:] = False   # padding past each sequence's end
+            keep[..., 7::11] = False  # and scattered holes
+            keep = keep.to(cuda)
+            vnan = v.clone()
+            vnan[:, :, ~keep[0, 0, 0]] = float("nan")
+            vzero = v.clone()
+            vzero[:, :, ~keep[0, 0, 0]] = 0
+            got = bi.scaled_dot_product_attention(q, k, vnan, mask=keep)
+            want = bi.scaled_dot_product_attention(q, k, vzero, mask=keep)
+            assert torch.isfinite(got).all(), "%s B=%d qL=%d" % (dname, B, qL)
+            assert np.array_equal(bits(got), bits(want)), "%s B=%d qL=%d" % (dname, B, qL)
+
+
 def test_context_growth_chunked_prefill(cuda):
     """32/8 heads, D=128, bf16; KV grown 4000 -> 4200 with the
     new keys masked. A query row's result computed over the first N' keys must
