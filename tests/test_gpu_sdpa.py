@@ -75,13 +75,16 @@ def test_batch_invariance(cuda):
 
 
 @pytest.mark.parametrize("H,Hkv,D,batches", [(32, 8, 128, (1, 32, 64)),
-                                              (32, 4, 64, (1, 32, 64, 128))])
+                                              (32, 4, 64, (1, 32, 64, 128)),
+                                              (64, 1, 128, (1, 3, 300)),    # MQA: 64 columns per kv head
+                                              (16, 16, 256, (1, 8, 20))])
 def test_head_grouping_does_not_change_bits(cuda, H, Hkv, D, batches):
-    """The launch shape follows the grid: bf16/f16 decode batches that fill
-    the GPU give each wave all output dims of its query columns, smaller ones
-    split the dims over waves and workgroups (the fp32 kernel likewise groups
-    query heads per workgroup by grid size). The batch sizes here cross those
-    choices: a row's bits must not move."""
+    """The launch shape follows the grid: bf16/f16 decode grids that fill the
+    GPU run one workgroup per kv head, smaller ones split the output dims over
+    2, 4 or 8 workgroups, and more than 16 query columns per kv head (MQA)
+    take the prefill shape; the fp32 kernel groups query heads per workgroup
+    by grid size. The batch sizes here cross those choices: a row's bits must
+    not move."""
     N = 256
     for dname, dtype in DTYPES:
         q1 = rn((1, H, 1, D), dtype, 31, device=cuda)
@@ -307,6 +310,11 @@ def test_closed_forms(cuda):
         y = bi.scaled_dot_product_attention(rn((1, 4, 8, 128), dtype, 87, device=cuda),
                                             kk[:, :, :5], vv[:, :, :5], mask="causal")
         assert (y[:, :, :3] == 0).all() and bool((y[:, :, 3:] != 0).any())
+        # No keys at all (an empty cache): every row is 0, with or without a sink.
+        e = torch.empty(1, 2, 0, 128, dtype=dtype, device=cuda)
+        assert (bi.scaled_dot_product_attention(qq, e, e) == 0).all()
+        assert (bi.scaled_dot_product_attention(qq, e, e, sinks=torch.ones(4, dtype=dtype,
+                                                                           device=cuda)) == 0).all()
         # A dominant sink drives the output to ~0.
         sinks = torch.full((4,), 60.0, dtype=dtype, device=cuda)
         y = f64(bi.scaled_dot_product_attention(qq, kk, vv, sinks=sinks))
