@@ -20,7 +20,8 @@
 //     mask_i > -3e38 (array mask) (reference :92-96).
 //   * Each chain runs an online softmax in base 2 over its blocks: with M the
 //     largest used score of the block (none: the block leaves the chain
-//     unchanged), m' = max(m, M), f = m' == m ? 1 : exp2(m - m'),
+//     unchanged), m' = M > m + 8 ? M : m (a lazily moved base: p <= 2^8),
+//     f = m' == m ? 1 : exp2(m - m'),
 //     p_i = exp2(s_i - m') (0 for unused keys), l = fma(l, f, sum_i p_i) with
 //     the block sum taken in a fixed tree; o = o * f + 0.0 (skipped when
 //     f == 1, which changes no bits), then o += p . v as v_mfma_f32_16x16x16 with p
@@ -354,7 +355,8 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   int64_t t = xcd_remap(blockIdx.x, (int)(p.B * p.Hkv * ncb * WS));
   const int ws = (int)(t % WS);
   t /= WS;
-  const int64_t cb = t % ncb;
+  // Causal: the last column blocks see the most keys; they start first.
+  const int64_t cb = p.mask_mode == BI_MASK_CAUSAL ? ncb - 1 - t % ncb : t % ncb;
   t /= ncb;
   const int64_t kvh = t % p.Hkv;
   const int64_t b = t / p.Hkv;
@@ -483,7 +485,9 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
         }
       bm = col_max(bm);
       const bool any = bm > -INFINITY;
-      const float mn = any ? fmaxf(m[ct], bm) : m[ct];
+      // The base moves only when the block's largest score passes it by more
+      // than 8 (p then stays <= 2^8): few rescales, the same result after o / l.
+      const float mn = (any && bm > m[ct] + 8.f) ? bm : m[ct];
       f[ct] = mn == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - mn);
       float pv[2][4];
       float ps = 0.f;
