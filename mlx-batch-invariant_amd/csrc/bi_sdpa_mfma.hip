@@ -25,7 +25,8 @@
 //     p_i = exp2(s_i - m') (0 for unused keys), l = fma(l, f, sum_i p_i) with
 //     the block sum taken in a fixed tree; o = o * f + 0.0 (skipped when
 //     f == 1, which changes no bits), then o += p . v as v_mfma_f32_16x16x16 with p
-//     split into hi = T(p) and lo = T(p - hi): for each 16-dim block, keys
+//     split into hi and lo = T(p - hi), hi = p truncated to bf16 (bf16) or
+//     T(p) (f16): for each 16-dim block, keys
 //     0-15 hi, keys 0-15 lo, keys 16-31 hi, keys 16-31 lo. m starts at the
 //     lowest finite float and l at 0; a sink starts chain 0 at m =
 //     sink * log2 e, l = 1 (reference :80-86).
@@ -40,6 +41,8 @@
 #include <float.h>
 #include <math.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "bi_internal.h"
 #include "bi_sdpa_args.h"
@@ -128,6 +131,40 @@ __device__ __forceinline__ u32x4_t ds_read_b128(uint32_t lds_addr) {
 
 template <typename T> __device__ inline unsigned short tbits(T x) {
   return __builtin_bit_cast(unsigned short, x);
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Splits four probabilities p (finite, >= 0) into two 16-bit planes packed
+// two per dword, element e in bits 16 (e % 2) of dword e / 2: hi + lo = p to
+// about 16 significant bits. bf16: hi is p's upper 16 bits (p truncated, so
+// p - hi is exact) and lo = RNE(p - hi). f16: hi = RNE(p), lo = RNE(p - hi).
+template <typename T>
+__device__ __forceinline__ void split_p(const float (&pv)[4], uint2& ph, uint2& pl) {
+  if constexpr (__is_same(T, __bf16)) {
+    uint32_t h[2], lo[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const uint32_t b0 = __float_as_uint(pv[2 * j]), b1 = __float_as_uint(pv[2 * j + 1]);
+      h[j] = __builtin_amdgcn_perm(b1, b0, 0x07060302);
+      const f32x2_t d = {pv[2 * j] - __uint_as_float(b0 & 0xFFFF0000u),
+                         pv[2 * j + 1] - __uint_as_float(b1 & 0xFFFF0000u)};
+      lo[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(d, bf16x2_t));
+    }
+    ph = make_uint2(h[0], h[1]);
+    pl = make_uint2(lo[0], lo[1]);
+  } else {
+    unsigned short hb[4], lb[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const T hi = (T)pv[e];
+      hb[e] = tbits(hi);
+      lb[e] = tbits((T)(pv[e] - (float)hi));
+    }
+    ph = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
+    pl = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
+  }
 }
 
 __device__ inline int xcd_remap(int w, int total) {
@@ -371,6 +408,7 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   };
   const int64_t last_cc = (c0 + COLS < ncol ? c0 + COLS : ncol) - 1;
   const int64_t nblk = (kend_of(last_cc / G) + kBlk - 1) / kBlk;
+  const int64_t kfull = kend_of(c0 / G);  // keys every column of the workgroup sees
 
   // This lane's column in each tile; its query as the B operand of the score
   // MFMAs (Q[col][32i + 8g ..]); its chain state.
@@ -454,67 +492,67 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
     uint2 ph[CT][2], pl[CT][2];
     float f[CT];
     uint32_t used = 0;  // mask: bit 4kt + e set if this lane's column uses key 16kt + 4g + e
+    // FULL: every column of the workgroup uses all 32 keys of the block (no
+    // mask, below every causal bound), so the per-key bookkeeping drops out;
+    // the arithmetic is the same.
+    auto softmax = [&](auto full_tag) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++) {
-      float s[2][4];
-      bool use[2][4];
-#pragma unroll
-      for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          s[kt][e] = sc[ct][kt][e] * p.scale2;
-          use[kt][e] = key0 + 16 * kt + e < kend[ct];
-        }
-      if constexpr (MK) {  // keys past N read 0 and are unused
+      for (int ct = 0; ct < CT; ct++) {
+        float s[2][4];
+        bool use[2][4];
 #pragma unroll
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            const float mv = (float)__builtin_bit_cast(T, mk[ct][4 * kt + e]);
-            use[kt][e] = use[kt][e] && mv > -3.0e38f;
-            s[kt][e] = s[kt][e] + mv * kLog2e;
+            s[kt][e] = sc[ct][kt][e] * p.scale2;
+            use[kt][e] = FULL || key0 + 16 * kt + e < kend[ct];
           }
+        if constexpr (MK) {  // keys past N read 0 and are unused
+#pragma unroll
+          for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const float mv = (float)__builtin_bit_cast(T, mk[ct][4 * kt + e]);
+              use[kt][e] = use[kt][e] && mv > -3.0e38f;
+              s[kt][e] = s[kt][e] + mv * kLog2e;
+            }
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
+            if constexpr (MK != 0) used |= use[kt][e] ? 1u << (4 * kt + e) : 0u;
+          }
+        bm = col_max(bm);
+        const bool any = bm > -INFINITY;
+        // The base moves only when the block's largest score passes it by more
+        // than 8 (p then stays <= 2^8): few rescales, the same result after o / l.
+        const float mn = (any && bm > m[ct] + 8.f) ? bm : m[ct];
+        f[ct] = mn == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - mn);
+        float pv[2][4];
+        float ps = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(s[kt][e] - mn) : 0.f;
+            ps = ps + pv[kt][e];
+          }
+        ps = col_sum(ps);
+        l[ct] = __builtin_fmaf(l[ct], f[ct], ps);
+        m[ct] = mn;
+        // P^T as the B operand of the 16x16x16 MFMAs, split into two planes.
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) split_p<T>(pv[kt], ph[ct][kt], pl[ct][kt]);
       }
-      float bm = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
-          if constexpr (MK != 0) used |= use[kt][e] ? 1u << (4 * kt + e) : 0u;
-        }
-      bm = col_max(bm);
-      const bool any = bm > -INFINITY;
-      // The base moves only when the block's largest score passes it by more
-      // than 8 (p then stays <= 2^8): few rescales, the same result after o / l.
-      const float mn = (any && bm > m[ct] + 8.f) ? bm : m[ct];
-      f[ct] = mn == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - mn);
-      float pv[2][4];
-      float ps = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(s[kt][e] - mn) : 0.f;
-          ps = ps + pv[kt][e];
-        }
-      ps = col_sum(ps);
-      l[ct] = __builtin_fmaf(l[ct], f[ct], ps);
-      m[ct] = mn;
-      // P^T as the B operand of the 16x16x16 MFMAs, split into two planes.
-#pragma unroll
-      for (int kt = 0; kt < 2; kt++) {
-        unsigned short hb[4], lb[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const T hi = (T)pv[kt][e];
-          hb[e] = tbits(hi);
-          lb[e] = tbits((T)(pv[kt][e] - (float)hi));
-        }
-        ph[ct][kt] = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
-        pl[ct][kt] = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
-      }
-    }
+    };
+    if (!MK && (blk + 1) * kBlk <= kfull)
+      softmax(std::true_type{});
+    else
+      softmax(std::false_type{});
     // Rescale; adding +0.0 turns an underflowed -0.0 into +0.0, so o is never
     // -0.0 and a column with no usable key in this block (f == 1, all p == 0)
     // keeps its o exactly through the products below.
