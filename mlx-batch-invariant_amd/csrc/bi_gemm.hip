@@ -40,6 +40,8 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int pick_geometry(int64_t M, int64_t N, int dtype) {
   if (M <= 16) return 0;
   if (M <= 64) return 1;
+  // Small outputs (e.g. 256 x 512): 64 x 64 tiles would leave most CUs idle.
+  if (ceil_div(M, 64) * ceil_div(N, 64) < 64) return 1;
   // fp32 carries two accumulator chains: the 256 x 128 footprint would need
   // more than the 256 registers a wave of an 8-wave workgroup can hold.
   if (dtype != BI_F32 && ceil_div(M, 256) * ceil_div(N, 128) >= 200) return 4;

@@ -999,7 +999,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
 #define BI_GEOMETRIES(X)                  \
   X(0, 16, 16, 1, 1, 4, 512, 6)           \
   X(1, 64, 16, 4, 1, 4, 256, 4)           \
-  X(2, 64, 64, 2, 2, 4, 256, 3)           \
+  X(2, 64, 64, 2, 2, 8, 256, 4)           \
   X(3, 128, 128, 4, 2, 8, 128, 4)         \
   X(4, 256, 128, 4, 2, 8, 128, 3)
 
