@@ -8,7 +8,8 @@ the sweep, (256, K) bf16 activations ~ N(0, 1) times (K, N) bf16 weights
 ~ N(0, 1/K), seeded. `value` is the step's total flops / wall time, inputs
 resident in HBM. Alongside, on the same run:
   * roofline of the dominant kernel (256 x 4096 x 32000), its average
-    duration measured with HIP events on the launch stream;
+    duration over the timed steps from HIP events that the launch itself
+    records (the kernel's own start and end timestamps);
   * stock torch.matmul (hipBLASLt) on the same inputs, interleaved;
   * decode SDPA (configs[2]: B = 64, 32/8 heads, D = 128, N = 8192) GB/s;
   * causal prefill SDPA (B = 1, 32/8 heads, D = 128, 2048 x 2048) TFLOP/s,
@@ -186,18 +187,22 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # Timed region: exactly --steps steps, synchronised on both sides; the
-    # dominant kernel is bracketed by events on the launch stream.
+    # Timed region: exactly --steps steps, synchronised on both sides. The
+    # dominant kernel's launch records its own start and end timestamps into a
+    # pair of HIP events (bi_gemm_timed, same kernel and arguments as
+    # bi.matmul): event markers between the launches would idle the GPU for
+    # several microseconds each and be counted in the kernel's time.
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
+    for e0, e1 in evs:  # torch creates the underlying HIP event on its first record
+        e0.record()
+        e1.record()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
         for i, (_, _, a, w) in enumerate(ops):
             if i == dom:
-                evs[s][0].record()
-                bi.matmul(a, w)
-                evs[s][1].record()
+                _gemm.matmul_timed(a, w, *evs[s])
             else:
                 bi.matmul(a, w)
     torch.cuda.synchronize()

@@ -35,6 +35,16 @@ int bi_gemm_with_geometry(const void* a, const void* b, const void* bias, void* 
                           int64_t M, int64_t N, int64_t K, int dtype, int trans_b,
                           float alpha, float beta, int g, void* hip_stream);
 
+/* bi_gemm (same arguments, semantics and kernel), with the kernel's own start
+ * and end timestamps recorded into `start_event` and `stop_event` (hipEvent_t,
+ * created by the caller; either may be NULL). A benchmark can then time one
+ * launch with no marker packets between kernels; a hipEventRecord on each side
+ * of a launch idles the GPU for several microseconds per record on this stack.
+ * The reference times host-side (bench/bench.py:32-49) and has no counterpart. */
+int bi_gemm_timed(const void* a, const void* b, const void* bias, void* out, int64_t M,
+                  int64_t N, int64_t K, int dtype, int trans_b, float alpha, float beta,
+                  void* start_event, void* stop_event, void* hip_stream);
+
 /* bi_qgemm with the geometry forced to `g` (same arguments and semantics). */
 int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
                            const void* biases, void* out, int64_t M, int64_t N, int64_t K,

@@ -2,6 +2,7 @@
 // argument validation and the C ABI entry points of include/bi.h and
 // include/bi_testing.h. The kernels and their arithmetic contract are in
 // bi_gemm_kernel.h.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -86,8 +87,12 @@ VecFlags vec_flags(const void* a, const void* b, int64_t N, int64_t K, int dtype
   return v;
 }
 
+// start/stop (optional): hipEvents that receive the dispatch's own start and
+// end timestamps (hipExtLaunchKernelGGL), so timing a launch adds no marker
+// packets around it.
 int launch(const void* a, const void* b, const void* bias, void* out, int64_t M, int64_t N,
-           int64_t K, int dtype, int trans_b, float alpha, float beta, int g, void* stream) {
+           int64_t K, int dtype, int trans_b, float alpha, float beta, int g, void* stream,
+           void* start = nullptr, void* stop = nullptr) {
   const Geometry& G = kGeometries[g];
   GemmArgs p;
   p.a = a;
@@ -108,8 +113,13 @@ int launch(const void* a, const void* b, const void* bias, void* out, int64_t M,
   if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_gemm: too many tiles");
   KernelFn fn = select_kernel(dtype, trans_b, g);
   if (!fn) return bi::fail(BI_EUNSUPPORTED, "bi_gemm: geometry %d not built for this dtype", g);
-  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * G.waves), 0,
-                     static_cast<hipStream_t>(stream), p);
+  if (start || stop)
+    hipExtLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * G.waves), 0,
+                          static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(start),
+                          static_cast<hipEvent_t>(stop), 0, p);
+  else
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * G.waves), 0,
+                       static_cast<hipStream_t>(stream), p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return bi::launch_error(e, "bi_gemm launch");
   return BI_OK;
@@ -124,6 +134,15 @@ extern "C" int bi_gemm(const void* a, const void* b, const void* bias, void* out
   if (rc != BI_OK || M == 0 || N == 0) return rc;
   return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta, pick_geometry(M, N, dtype),
                 hip_stream);
+}
+
+extern "C" int bi_gemm_timed(const void* a, const void* b, const void* bias, void* out,
+                             int64_t M, int64_t N, int64_t K, int dtype, int trans_b, float alpha,
+                             float beta, void* start_event, void* stop_event, void* hip_stream) {
+  const int rc = validate(a, b, out, M, N, K, dtype, trans_b);
+  if (rc != BI_OK || M == 0 || N == 0) return rc;
+  return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta, pick_geometry(M, N, dtype),
+                hip_stream, start_event, stop_event);
 }
 
 extern "C" int bi_gemm_num_geometries(void) { return kNumGeometries; }

@@ -65,7 +65,7 @@ def _gemm(a, b, bias, transpose_b, alpha=1.0, beta=1.0, geometry=None):
     return _gemm_eager(a, b, bias, transpose_b, alpha, beta, geometry)
 
 
-def _gemm_eager(a, b, bias, transpose_b, alpha=1.0, beta=1.0, geometry=None):
+def _gemm_eager(a, b, bias, transpose_b, alpha=1.0, beta=1.0, geometry=None, events=None):
     if a.dtype != b.dtype:
         raise ValueError("a and b must share a dtype, got %s and %s" % (a.dtype, b.dtype))
     if a.ndim < 2 or b.ndim != 2:
@@ -112,18 +112,28 @@ def _gemm_eager(a, b, bias, transpose_b, alpha=1.0, beta=1.0, geometry=None):
         stream, switch = _lib.launch_stream(a.device)
         if switch:
             with torch.cuda.device(a.device):
-                rc = _launch(L, args, geometry, stream)
+                rc = _launch(L, args, geometry, stream, events)
         else:
-            rc = _launch(L, args, geometry, stream)
+            rc = _launch(L, args, geometry, stream, events)
         if rc:
             _lib.check(rc, "bi_gemm")
     return out if len(lead) == 1 else out.reshape(*lead, N)
 
 
-def _launch(L, args, geometry, stream):
+def _launch(L, args, geometry, stream, events=None):
+    if events is not None:
+        return L.bi_gemm_timed(*args, events[0].cuda_event, events[1].cuda_event, stream)
     if geometry is None:
         return L.bi_gemm(*args, stream)
     return L.bi_gemm_with_geometry(*args, int(geometry), stream)
+
+
+def matmul_timed(a, b, start, stop):
+    """matmul(a, b) whose kernel records its own start and end timestamps into
+    the torch.cuda.Events `start` and `stop` (bi_gemm_timed): times one launch
+    without event markers between kernels. Both events must have been recorded
+    once before (torch creates the underlying event on its first record)."""
+    return _gemm_eager(a, b, None, False, events=(start, stop))
 
 
 def matmul(a, b):

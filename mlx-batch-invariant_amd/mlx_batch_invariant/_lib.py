@@ -42,6 +42,8 @@ SIGNATURES = {
     "bi_gemm_pick_geometry": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "bi_gemm_with_geometry": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                                        _c_int, _c_int, _c_float, _c_float, _c_int, _c_vp]),
+    "bi_gemm_timed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
+                               _c_int, _c_float, _c_float, _c_vp, _c_vp, _c_vp]),
     "bi_qgemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                           _c_int, _c_int, _c_vp]),
     "bi_qgemm_with_geometry": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,

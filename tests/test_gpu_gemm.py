@@ -289,3 +289,18 @@ def test_wavefront_is_64(cuda):
     w = ctypes.c_int()
     _lib.check(_lib.lib().bi_device_wavefront_size(ctypes.byref(w)), "wavefront")
     assert w.value == 64
+
+
+def test_timed_launch_matches_and_records_the_kernel(cuda):
+    """bi_gemm_timed runs the same kernel as bi_gemm (same bits) and writes the
+    launch's own start/end timestamps into the two events."""
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(256, 4096, generator=g).to(torch.bfloat16).to(cuda)
+    b = (torch.randn(4096, 4096, generator=g) / 64).to(torch.bfloat16).to(cuda)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    e1.record()
+    y = _gemm.matmul_timed(a, b, e0, e1)
+    torch.cuda.synchronize()
+    assert (bits(y) == bits(bi.matmul(a, b))).all()
+    assert 0.0 < e0.elapsed_time(e1) < 100.0  # milliseconds
