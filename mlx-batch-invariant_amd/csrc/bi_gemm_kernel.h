@@ -150,12 +150,28 @@ __device__ inline uint4 buffer_chunk(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 }
 
 // Chunk swizzles: 16-byte chunk c of LDS row r is stored at chunk position
-// c ^ swz(r) so that the MFMA operand reads of 16 consecutive rows spread over
-// the LDS banks.
-__device__ inline int swz_k(int r) { return r & 7; }  // [rows][>= 8 chunks] tiles
+// c ^ swz(r) so that the MFMA operand reads spread over the LDS banks. The LDS
+// has 64 banks of 4 bytes (256 bytes); by the bank-conflict counter, a 16-byte
+// read serves lanes 0-7 and 16-23 in one pass (then 8-15 and 24-31, ...), i.e.
+// rows 0-7 of a 16-row operand block at chunks 4j + g and 4j + g + 1. Rows of
+// 8 chunks (128 bytes) put row parity in the bank half, so c ^ (r & 7) covers
+// the 16 bank groups; rows of 16 or more chunks need c ^ 2 (r & 7), which sends
+// the two chunks to even and odd bank groups (c ^ (r & 7) would give both chunk
+// sets the same 8 bank groups: a 2-way conflict on every read).
+template <int RC>
+__device__ inline int swz_k(int r) {  // [rows][RC >= 8 chunks] tiles
+  return RC >= 16 ? (r & 7) << 1 : r & 7;
+}
+// (K, N) B tiles are read with ds_read_b64_tr_b16: lane group g reads k-rows
+// 8g + (0..3) (plus 4 for the second half), 32 bytes each. One pass serves
+// groups 0 and 1 (then 2 and 3), 8 rows. 256-byte rows (16 chunks): the row's
+// low two bits and bit 3 pick one of 8 chunk pairs. 128-byte rows (8 chunks):
+// row parity picks the bank half, so bits 1 and 3 pick one of 4 chunk pairs.
 template <typename T, int CPR>
 __device__ inline int swz_nn(int k) {  // [k][CPR chunks] tiles (B in (K, N) layout)
-  if constexpr (sizeof(T) == 2)
+  if constexpr (sizeof(T) == 2 && CPR == 8)
+    return (((k >> 1) & 1) << 1) | (((k >> 3) & 1) << 2);
+  else if constexpr (sizeof(T) == 2)
     return (((k & 3) << 1) | (((k >> 3) & 1) << 3)) & (CPR - 1);
   else
     return (((k >> 2) & 3) << 2) & (CPR - 1);
@@ -235,8 +251,8 @@ struct GemmTile {
   __device__ __forceinline__ void init_lds_offsets() {
 #pragma unroll
     for (int j = 0; j < CS; j++) {
-      int ao = (wm * WTM + r16) * RC + ((4 * j + g) ^ swz_k(r16));
-      int bo = (wn * WTN + r16) * RC + ((4 * j + g) ^ swz_k(r16));
+      int ao = (wm * WTM + r16) * RC + ((4 * j + g) ^ swz_k<RC>(r16));
+      int bo = (wn * WTN + r16) * RC + ((4 * j + g) ^ swz_k<RC>(r16));
       asm("" : "+v"(ao));
       asm("" : "+v"(bo));
       a_off[j] = ao;
@@ -273,7 +289,7 @@ struct GemmTile {
     for (int i = 0; i < DMA; i++) {
       const int p = dma_blk(i) * 64 + lane;  // chunk position within the A or B region
       if (i < DMA_A || TB) {
-        const int r = p / RC, c = (p % RC) ^ swz_k(r);
+        const int r = p / RC, c = (p % RC) ^ swz_k<RC>(r);
         dma_base[i] = (uint32_t)(r * K + c * EPC) * E;
         dma_kidx[i] = c * EPC;
       } else {
@@ -330,7 +346,7 @@ struct GemmTile {
       const int q = tid + i * NT;
       if (A_CH % NT == 0 || q < A_CH) {
         const int r = q / RC, c = q % RC;
-        As[r * RC + (c ^ swz_k(r))] = ra[i];
+        As[r * RC + (c ^ swz_k<RC>(r))] = ra[i];
       }
     }
 #pragma unroll
@@ -339,7 +355,7 @@ struct GemmTile {
       if (B_CH % NT == 0 || q < B_CH) {
         if constexpr (TB) {
           const int r = q / RC, c = q % RC;
-          Bs[r * RC + (c ^ swz_k(r))] = rb[i];
+          Bs[r * RC + (c ^ swz_k<RC>(r))] = rb[i];
         } else {
           const int r = q / NN_CPR, c = q % NN_CPR;
           Bs[r * NN_CPR + (c ^ swz_nn<T, NN_CPR>(r))] = rb[i];
@@ -642,7 +658,7 @@ struct GemmTile {
       const int q = tid + i * NT;
       if (A_CH % NT == 0 || q < A_CH) {
         const int r = q / RC, c = q % RC;
-        sl.a[r * RC + (c ^ swz_k(r))] = st.a[i];
+        sl.a[r * RC + (c ^ swz_k<RC>(r))] = st.a[i];
       }
     }
 #pragma unroll
@@ -659,7 +675,7 @@ struct GemmTile {
           v.y = pack_codes(code_at(d, 8 * cc + 2), code_at(d, 8 * cc + 3));
           v.z = pack_codes(code_at(d, 8 * cc + 4), code_at(d, 8 * cc + 5));
           v.w = pack_codes(code_at(d, 8 * cc + 6), code_at(d, 8 * cc + 7));
-          sl.b[r * RC + ((c + cc) ^ swz_k(r))] = v;
+          sl.b[r * RC + ((c + cc) ^ swz_k<RC>(r))] = v;
         }
       }
     }
