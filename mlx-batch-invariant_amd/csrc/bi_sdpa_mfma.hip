@@ -243,11 +243,19 @@ struct Chain {
   // slot array exactly and its (m, l) fit in another.
   static_assert(kWaves * NB * 64 <= ARR_U4 && kWaves * 64 / 2 <= ARR_U4, "merge staging");
 
-  // Value slot: [32 keys][VCH chunks], chunk c of key r at c ^ swz_v(r):
-  // ds_read_tr16_b64 reads four consecutive keys of 16 dims, and the swizzle
-  // puts those rows on distinct banks.
+  // Value slot: [32 keys][VCH chunks], chunk c of key r at c ^ swz_v(r).
+  // ds_read_tr16_b64: lane group g reads keys 4g + (0..3), 16 dims (32 bytes,
+  // a chunk pair) each; by the bank-conflict counter one pass serves groups 0
+  // and 1 (then 2 and 3), i.e. 8 consecutive keys. The LDS has 64 banks of 4
+  // bytes; with RP keys per 256 bytes, XORing key r's chunk pairs with
+  // (r / RP) mod (pairs per row, at most 8) puts those 8 keys on distinct banks.
   __device__ __forceinline__ static int swz_v(int r) {
-    return ((((r & 3) << 1) | (((r >> 3) & 1) << 3))) & (VCH - 1);
+    constexpr int ROWB = VCH * 16, RP = ROWB >= 256 ? 1 : 256 / ROWB;
+    constexpr int PB = ROWB / 32 < 8 ? ROWB / 32 : 8;
+    if constexpr (PB > 1)
+      return ((r / RP) & (PB - 1)) << 1;
+    else
+      return 0;
   }
   // Key slot (KL): [32 keys][CH chunks], chunk c of key r at c ^ swz_k(r): the
   // score MFMAs' A reads (16 keys, one chunk each) then hit distinct banks.
