@@ -911,11 +911,57 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
     t.main_loop_slow(slots, nst, nsteps, computes, acc);
   }
 
+  // Epilogue: one rounding per element. A wave whose sub-tile lies wholly
+  // inside C, with 16-byte aligned output rows, rounds its tile into LDS
+  // (the ring is free once every wave is past the loop and no load is in
+  // flight) and stores it back row by row with 16-byte stores, so each row
+  // of the tile is written as whole cache lines. Otherwise (C's edges,
+  // unaligned rows) each lane stores its own elements. Both store the same
+  // values.
+  constexpr int SWB = Tile::WTM * Tile::WTN * (int)sizeof(T);  // staged bytes per wave
+  constexpr int WPA = AC * 16 / SWB;                            // waves per A array
+  constexpr bool STAGED = WPA >= 1 && WPA * NS >= Tile::CW;
+  if constexpr (STAGED) {
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("s_barrier" ::: "memory");
+  }
   if (!computes) return;
-  // Epilogue: one rounding per element.
   T* __restrict__ out = static_cast<T*>(p.out);
   const T* __restrict__ bias = static_cast<const T*>(p.bias);
   const float alpha = p.alpha, beta = p.beta;
+  if constexpr (STAGED) {
+    const bool whole = wrow + Tile::WTM <= M && wcol + Tile::WTN <= N &&
+                       N % Tile::EPC == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    if (whole) {
+      T* stage = reinterpret_cast<T*>(slots(t.wave / WPA).a) + (t.wave % WPA) * (SWB / (int)sizeof(T));
+#pragma unroll
+      for (int jn = 0; jn < FN; jn++) {
+        const int c = jn * 16 + t.r16;
+        const float bv = bias ? beta * Elem<T>::to_f32(bias[wcol + c]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            float v = acc[0][i][jn][e];
+            if constexpr (CHAINS == 2) v = v + acc[1][i][jn][e];
+            if (bias) v = __builtin_fmaf(alpha, v, bv);
+            stage[(i * 16 + 4 * t.g + e) * Tile::WTN + c] = Elem<T>::from_f32(v);
+          }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      constexpr int CPRW = Tile::WTN * (int)sizeof(T) / 16;  // 16-byte chunks per tile row
+      constexpr int RPI = 64 / CPRW;                          // rows per wave-wide pass
+#pragma unroll
+      for (int r0 = 0; r0 < Tile::WTM; r0 += RPI) {
+        const int r = r0 + t.lane / CPRW, c = t.lane % CPRW;
+        if (RPI <= Tile::WTM || r < Tile::WTM) {
+          const uint4 v = reinterpret_cast<const uint4*>(stage)[r * CPRW + c];
+          *reinterpret_cast<uint4*>(out + (wrow + r) * N + wcol + c * Tile::EPC) = v;
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int jn = 0; jn < FN; jn++) {
     const int64_t col = wcol + jn * 16 + t.r16;
