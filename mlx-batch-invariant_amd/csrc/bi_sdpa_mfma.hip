@@ -734,10 +734,11 @@ struct Shape {
 
 // Shapes: "rows" (two column tiles per workgroup, one for D = 256; mask
 // values loaded in their own block, for registers) when a kv head has more
-// than 16 columns (prefill); otherwise one column tile, with the dims split
-// over WS workgroups when the decode grid would leave compute units idle (and
-// always at least in two for D = 256). Keys one
-// block ahead and values in two slots: deeper prefetch measured no faster.
+// than 16 columns (prefill) and that grid fills the compute units; otherwise
+// one column tile, with the dims split over WS workgroups when the grid of
+// column tiles would leave compute units idle (and always at least in two for
+// D = 256): decode, and short chunks of prefill such as 16 query rows. Keys
+// one block ahead and values in two slots: deeper prefetch measured no faster.
 template <typename T, int D, bool MASK>
 Shape shape_for(int64_t ncol, int64_t streams, int cus) {
   constexpr int CT_ROWS = D == 256 ? 1 : 2;
@@ -750,10 +751,13 @@ Shape shape_for(int64_t ncol, int64_t streams, int cus) {
   // (measured faster for D = 128 only; D = 256 key slots would not fit LDS).
   constexpr bool KLS = !MASK && D == 128;
   constexpr int PKS_ = KLS ? 0 : PK, SVS_ = KLS ? 3 : 2;
-  if (ncol > 16) return {sdpa_mfma_kernel<T, D, CT_ROWS, PK, 2, WS1, MK_ROWS, false>, 16 * CT_ROWS, WS1};
-  if (streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS1, MK, false>, 16, WS1};
-  if (2 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 2, MK, KLS>, 16, 2};
-  if (4 * streams >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 4, MK, KLS>, 16, 4};
+  const int64_t rows_grid = streams * ((ncol + 16 * CT_ROWS - 1) / (16 * CT_ROWS));
+  if (ncol > 16 && rows_grid >= cus)
+    return {sdpa_mfma_kernel<T, D, CT_ROWS, PK, 2, WS1, MK_ROWS, false>, 16 * CT_ROWS, WS1};
+  const int64_t tiles = streams * ((ncol + 15) / 16);  // workgroups at one column tile
+  if (tiles >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS1, MK, false>, 16, WS1};
+  if (2 * tiles >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 2, MK, KLS>, 16, 2};
+  if (4 * tiles >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 4, MK, KLS>, 16, 4};
   return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, WS8, MK, KLS>, 16, WS8};
 }
 
