@@ -39,8 +39,12 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // thresholds come from measurements of this table on MI355X; since every
 // geometry computes the same bits, they only move time.
 int pick_geometry(int64_t M, int64_t N, int dtype) {
+  // Decode: 16 x 16 tiles in a 64 KB ring, two workgroups per CU, so one
+  // workgroup's ramp-up overlaps another's streaming (M = 1: 7 TB/s on a
+  // 4096 x 32000 weight).
   if (M <= 16) return 0;
-  if (M <= 64) return 1;
+  // 17..64 rows: 64 x 32 tiles (8 waves) once they still fill the CUs.
+  if (M <= 64) return ceil_div(N, 32) >= 256 ? 5 : 1;
   // Small outputs (e.g. 256 x 512): 64 x 64 tiles would leave most CUs idle.
   if (ceil_div(M, 64) * ceil_div(N, 64) < 64) return 1;
   // fp32 carries two accumulator chains: the 256 x 128 footprint would need
@@ -266,6 +270,7 @@ extern "C" int bi_qgemm(const void* x, const void* w, const void* scales, const 
   // loads in flight; 128 x 128 takes its place.
   int g = pick_geometry(M, N, dtype);
   if (g == 4) g = 3;
+  if (g == 5) g = 1;  // the quantized kernel keeps 64 x 16 for 17..64 rows
   return qlaunch(x, w, scales, biases, out, M, N, K, group_size, bits, dtype, g, hip_stream);
 }
 

@@ -1059,11 +1059,12 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
 // latency hiding. Columns: id, BM, BN, WM, WN, NW (waves), KB (stage bytes),
 // NS (LDS ring stages).
 #define BI_GEOMETRIES(X)                  \
-  X(0, 16, 16, 1, 1, 4, 512, 6)           \
+  X(0, 16, 16, 1, 1, 4, 512, 4)           \
   X(1, 64, 16, 4, 1, 4, 256, 4)           \
   X(2, 64, 64, 2, 2, 8, 256, 4)           \
   X(3, 128, 128, 4, 2, 8, 128, 4)         \
-  X(4, 256, 128, 4, 2, 8, 128, 3)
+  X(4, 256, 128, 4, 2, 8, 128, 3)         \
+  X(5, 64, 32, 4, 2, 8, 256, 3)
 
 using KernelFn = void (*)(GemmArgs);
 
