@@ -40,7 +40,7 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // geometry computes the same bits, they only move time.
 int pick_geometry(int64_t M, int64_t N, int dtype) {
   // Decode: 16 x 16 tiles in a 64 KB ring, two workgroups per CU, so one
-  // workgroup's ramp-up overlaps another's streaming (M = 1: 7 TB/s on a
+  // workgroup's ramp-up overlaps another's streaming (M = 1: 6.8 TB/s on a
   // 4096 x 32000 weight).
   if (M <= 16) return 0;
   // 17..64 rows: 64 x 32 tiles (8 waves) once they still fill the CUs.

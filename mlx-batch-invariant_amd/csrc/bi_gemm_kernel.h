@@ -954,7 +954,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int r0 = 0; r0 < Tile::WTM; r0 += RPI) {
         const int r = r0 + t.lane / CPRW, c = t.lane % CPRW;
-        if (RPI <= Tile::WTM || r < Tile::WTM) {
+        if (Tile::WTM % RPI == 0 || r < Tile::WTM) {
           const uint4 v = reinterpret_cast<const uint4*>(stage)[r * CPRW + c];
           *reinterpret_cast<uint4*>(out + (wrow + r) * N + wcol + c * Tile::EPC) = v;
         }
