@@ -104,11 +104,32 @@ def cpu_baseline(ops):
             flops += gemm_flops(CPU_ROWS, a32.shape[1], bt.shape[0])
         passes += 1
     dt = time.perf_counter() - t0
+
+    # Beside it: stock torch on the CPU (fp32 matmul, same rows and shapes) and
+    # the reference's own CPU backend, MLX, when it is importable.
+    import importlib.util
+
+    import torch
+
+    torch.set_num_threads(cores)
+    tt = [(torch.from_numpy(a32), torch.from_numpy(bt).t()) for a32, bt, _ in prepared]
+    tflops, tpasses = 0.0, 0
+    t1 = time.perf_counter()
+    while tpasses == 0 or time.perf_counter() - t1 < 2.0:
+        for a32, b32 in tt:
+            torch.matmul(a32, b32)
+            tflops += gemm_flops(CPU_ROWS, a32.shape[1], b32.shape[1])
+        tpasses += 1
+    tdt = time.perf_counter() - t1
+    mlx = importlib.util.find_spec("mlx") is not None
     return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": cores,
             "kind": "port",
             "sample": "%d pass(es) over the first %d of the %d rows of each of the 5 (K,N) "
                       "shapes; fixed-order fp32 fmaf restatement of the reference K loop "
-                      "(oracle/csrc/oracle.c), %.1f s" % (passes, CPU_ROWS, M, dt)}
+                      "(oracle/csrc/oracle.c), %.1f s" % (passes, CPU_ROWS, M, dt),
+            "torch_cpu_tflops": round(tflops / tdt / 1e12, 4),
+            "mlx_cpu": ("mlx is importable but its CPU timing is not built in this bench"
+                        if mlx else "unavailable: mlx is not installed on this host")}
 
 
 def model_determinism(torch, bi, dev):
@@ -228,7 +249,9 @@ def main():
             bi_t.append(time_us(lambda: bi.matmul(a, w)))
             st_t.append(time_us(lambda: torch.matmul(a, w)))
         tb, ts = statistics.median(bi_t), statistics.median(st_t)
+        ratio = statistics.median(s_ / b_ for b_, s_ in zip(bi_t, st_t))
         per_shape.append({"M": M, "K": K, "N": N, "bi_us": round(tb, 2),
+                          "speedup_vs_stock": round(ratio, 3),
                           "bi_tflops": round(gemm_flops(M, K, N) / tb / 1e6, 1),
                           "stock_us": round(ts, 2),
                           "stock_tflops": round(gemm_flops(M, K, N) / ts / 1e6, 1),
