@@ -19,7 +19,7 @@ from . import _lib
 # tile (BM, BN, BK, SG_M, SG_N) as TILE (reference _gemm.py:25-27) and a test
 # pins it; this build pins the parts that decide an element's bits: the MFMA
 # shape, the K bytes per stage, the K chunk each lane group supplies, and the
-# epilogue. Workgroup footprints are listed separately in GEOMETRIES; they do
+# epilogue. Workgroup footprints are listed separately by geometries(); they do
 # not enter any element's arithmetic.
 TILE = dict(
     MFMA_16BIT="v_mfma_f32_16x16x32",   # bf16 / f16 inputs, fp32 accumulate
