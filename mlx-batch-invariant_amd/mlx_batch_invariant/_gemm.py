@@ -18,13 +18,13 @@ from . import _lib
 # Fixed per-element arithmetic of the kernel. The reference exports its single
 # tile (BM, BN, BK, SG_M, SG_N) as TILE (reference _gemm.py:25-27) and a test
 # pins it; this build pins the parts that decide an element's bits: the MFMA
-# shape, the K bytes per stage, the K chunk each lane group supplies, and the
-# epilogue. Workgroup footprints are listed separately by geometries(); they do
-# not enter any element's arithmetic.
+# shape, the K chunk each chunk-step consumes, the fp32 chain rule and the
+# epilogue. Workgroup footprints (and the K bytes each footprint stages per
+# pipeline step) are listed separately by geometries(); they do not enter any
+# element's arithmetic.
 TILE = dict(
     MFMA_16BIT="v_mfma_f32_16x16x32",   # bf16 / f16 inputs, fp32 accumulate
     MFMA_FP32="v_mfma_f32_16x16x4_f32",
-    BK_BYTES=128,                        # K per stage: 64 halfs or 32 floats
     K_CHUNK_16BIT=32,                    # K per MFMA for 16-bit inputs
     K_CHUNK_FP32=16,                     # K per chunk-step (4 MFMAs) for fp32
     FP32_CHAINS=2,                       # fp32: chunk-step j feeds chain j; acc = c0 + c1

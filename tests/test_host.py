@@ -106,7 +106,7 @@ def test_tile_contract_is_pinned():
     """Guard against anyone changing the per-element arithmetic (the analogue
     of reference tests/test_invariance.py:468-470)."""
     assert bi.TILE == dict(MFMA_16BIT="v_mfma_f32_16x16x32", MFMA_FP32="v_mfma_f32_16x16x4_f32",
-                           BK_BYTES=128, K_CHUNK_16BIT=32, K_CHUNK_FP32=16, FP32_CHAINS=2,
+                           K_CHUNK_16BIT=32, K_CHUNK_FP32=16, FP32_CHAINS=2,
                            EPILOGUE="fma(alpha, acc, beta * bias) then one RNE rounding")
     assert _attention.PARTIALS == 32 and _attention.GROUP_LANES == 8
     assert bi.HEAD_DIMS == (64, 128, 256)
