@@ -8,9 +8,13 @@
 // (_gemm.py:115-129). No split-K, no atomics.
 //
 // Fixed per-element arithmetic (the invariance contract):
-//   * K is consumed in chunk-steps q = 0, 1, 2, ... in ascending order, exactly
+//   * K is consumed in chunk-steps q = 0, 1, 2, ... in ascending order,
 //     ceil(K / 32) of them for bf16/f16 and ceil(K / 16) for fp32 -- a function
-//     of K alone. Elements past K read as zero.
+//     of K alone. Elements past K read as zero. The pipelined loop may run a
+//     few more chunk-steps to finish its last round of stages; those see only
+//     zeros in both operands, and adding exact zeros to an accumulator that
+//     starts at +0.0 changes no bit (it can never hold -0.0, and x + 0 = x for
+//     every other x, NaN and infinities included).
 //       bf16/f16: chunk-step q is one v_mfma_f32_16x16x32_{bf16,f16}; lane
 //                 group g = lane / 16 supplies k = 32q + 8g + t, t = 0..7.
 //       fp32:     chunk-step q is four v_mfma_f32_16x16x4_f32, t = 0..3; lane
@@ -468,15 +472,14 @@ struct GemmTile {
   // computing stage s, this wave's loads of stages s+1 .. s+NS-2 may still be
   // in flight, then a barrier makes every wave's part of stage s visible and
   // guarantees the slot about to be refilled is no longer read.
-  // The steady state has no branches: whole rounds of NS stages whose chunk-
-  // steps are all inside K. A tail round handles the partial last stage;
-  // stages past K load zeros and compute nothing.
+  // The loop has no branches: whole rounds of NS stages, every stage computed
+  // in full. Past K the stages hold zeros, which change no bit (file header).
+  // A workgroup whose waves all compute runs only this loop: a wave whose
+  // sub-tile lies outside C computes too and then stores nothing.
   template <bool COMPUTE, typename Slots>
-  __device__ __forceinline__ void dma_rounds(const Slots& slots, int64_t nst, int64_t nsteps,
+  __device__ __forceinline__ void dma_rounds(const Slots& slots, int64_t nst,
                                              f32x4_t (&acc)[CHAINS][FM][FN]) const {
-    const int64_t full_rounds = (nsteps / CS) / NS;
-    int64_t s0 = 0;
-    for (int64_t r = 0; r < full_rounds; r++, s0 += NS) {
+    for (int64_t s0 = 0; s0 < nst; s0 += NS) {
 #pragma unroll
       for (int u = 0; u < NS; u++) {
         __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DMA * (NS - 2)));
@@ -485,27 +488,17 @@ struct GemmTile {
         if constexpr (COMPUTE) compute_full(slots(u), acc);
       }
     }
-    for (; s0 < nst; s0 += NS) {
-#pragma unroll
-      for (int u = 0; u < NS; u++) {
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DMA * (NS - 2)));
-        asm volatile("s_barrier" ::: "memory");
-        dma(s0 + u + NS - 1, slots((u + NS - 1) % NS));
-        if constexpr (COMPUTE) compute(slots(u), steps_of(nsteps, s0 + u), acc);
-      }
-    }
   }
 
   template <typename Slots>
-  __device__ __forceinline__ void main_loop_dma(const Slots& slots, int64_t nst,
-                                                int64_t nsteps, bool computes,
+  __device__ __forceinline__ void main_loop_dma(const Slots& slots, int64_t nst, bool computes,
                                                 f32x4_t (&acc)[CHAINS][FM][FN]) const {
 #pragma unroll
     for (int u = 0; u < NS - 1; u++) dma(u, slots(u));
-    if (computes)
-      dma_rounds<true>(slots, nst, nsteps, acc);
+    if (NW == CW || computes)
+      dma_rounds<true>(slots, nst, acc);
     else
-      dma_rounds<false>(slots, nst, nsteps, acc);
+      dma_rounds<false>(slots, nst, acc);
   }
 
   // ---- Affine-quantized B (QB bits per weight; 16-bit elements only).
@@ -906,7 +899,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
   if (p.vec_a && p.vec_b) {
     t.init_buffers();
     t.init_dma();
-    t.main_loop_dma(slots, nst, nsteps, computes, acc);
+    t.main_loop_dma(slots, nst, computes, acc);
   } else {
     t.main_loop_slow(slots, nst, nsteps, computes, acc);
   }

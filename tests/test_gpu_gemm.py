@@ -304,3 +304,35 @@ def test_timed_launch_matches_and_records_the_kernel(cuda):
     torch.cuda.synchronize()
     assert (bits(y) == bits(bi.matmul(a, b))).all()
     assert 0.0 < e0.elapsed_time(e1) < 100.0  # milliseconds
+
+
+def test_padding_steps_change_no_bit(cuda):
+    """The pipelined loop finishes its last round of stages with chunk-steps
+    that see only zeros. Those add exact zeros to an accumulator that starts at
+    +0.0, so every footprint gives the same bits for ragged K, exact-zero sums
+    (which must stay +0.0), negative zeros in the inputs and infinities."""
+    geos = _gemm.geometries()
+    for dname, dtype in DTYPES:
+        for K in (520, 1000, 4104):
+            a = rn((70, K), dtype, 21, device=cuda)
+            b = rn((K, 96), dtype, 22, std=K ** -0.5, device=cuda)
+            a[0] = 0.0                     # all products zero
+            a[1] = -0.0
+            a[2, 0::2], a[2, 1::2] = 1.0, -1.0  # with b[:, 0] = 1: an exact-zero sum
+            b[:, 0] = 1.0
+            b[:, 1] = -0.0
+            a[3, 5] = float("inf")
+            outs = {}
+            for gi in range(len(geos)):
+                try:
+                    outs[gi] = bits(_gemm._gemm(a, b, None, False, geometry=gi))
+                except NotImplementedError:
+                    continue
+            ref = outs[0]
+            for gi, o in outs.items():
+                assert (o == ref).all(), "%s K=%d geometry %s differs" % (dname, K, geos[gi])
+            y = _gemm._gemm(a, b, None, False)
+            z = torch.zeros((), dtype=dtype, device=cuda)
+            for r, c in [(0, 0), (0, 7), (1, 3), (2, 0), (0, 1)]:
+                assert bits(y[r, c:c + 1])[0] == bits(z.reshape(1))[0], \
+                    "%s K=%d: element (%d, %d) is not +0.0" % (dname, K, r, c)
