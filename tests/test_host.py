@@ -50,6 +50,26 @@ def test_abi_version_and_geometry_table():
         assert 0 <= L.bi_gemm_pick_geometry(M, 4096, 4096, _lib.BF16, 1) < len(geos)
 
 
+def test_footprint_policy():
+    """The footprint bi_gemm picks for representative shapes (a performance
+    policy, measured on MI355X; every footprint gives the same bits, which the
+    GPU tests prove). Footprints are identified by (rows, columns, waves)."""
+    L = _lib.lib()
+    geos = bi.geometries()
+
+    def pick(M, N, dtype=_lib.BF16):
+        return geos[L.bi_gemm_pick_geometry(M, N, 4096, dtype, 1)]
+
+    assert pick(1, 4096) == pick(16, 32000) == (16, 16, 4)      # decode
+    assert pick(32, 11008) == pick(64, 32000) == (64, 32, 8)    # 17..64 rows, wide weight
+    assert pick(32, 4096) == (64, 16, 4)                        # 17..64 rows, narrow weight
+    assert pick(256, 512) == (64, 16, 4)                        # small output
+    assert pick(256, 4096) == (64, 64, 8)
+    assert pick(256, 11008) == (128, 128, 8)
+    assert pick(256, 32000) == (256, 128, 8)                    # the bench's dominant shape
+    assert pick(256, 32000, _lib.F32) == (128, 128, 8)          # fp32: registers
+
+
 def _err():
     return _lib.lib().bi_last_error().decode()
 
