@@ -732,8 +732,9 @@ struct Shape {
   int cols, ws;
 };
 
-// Shapes: "rows" (two column tiles per workgroup, one for D = 256; mask
-// values loaded in their own block, for registers) when a kv head has more
+// Shapes: "rows" (two column tiles per workgroup, one for D = 256; with an
+// array mask, mask values loaded in their own block and keys not loaded ahead,
+// which keeps two workgroups per CU within the registers) when a kv head has more
 // than 16 columns (prefill) and that grid fills the compute units; otherwise
 // one column tile, with the dims split over WS workgroups when the grid of
 // column tiles would leave compute units idle (and always at least in two for
@@ -753,7 +754,8 @@ Shape shape_for(int64_t ncol, int64_t streams, int cus) {
   constexpr int PKS_ = KLS ? 0 : PK, SVS_ = KLS ? 3 : 2;
   const int64_t rows_grid = streams * ((ncol + 16 * CT_ROWS - 1) / (16 * CT_ROWS));
   if (ncol > 16 && rows_grid >= cus)
-    return {sdpa_mfma_kernel<T, D, CT_ROWS, PK, 2, WS1, MK_ROWS, false>, 16 * CT_ROWS, WS1};
+    return {sdpa_mfma_kernel<T, D, CT_ROWS, MASK ? 0 : PK, 2, WS1, MK_ROWS, false>, 16 * CT_ROWS,
+            WS1};
   const int64_t tiles = streams * ((ncol + 15) / 16);  // workgroups at one column tile
   if (tiles >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS1, MK, false>, 16, WS1};
   if (2 * tiles >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 2, MK, KLS>, 16, 2};
