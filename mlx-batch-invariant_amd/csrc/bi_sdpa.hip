@@ -319,9 +319,12 @@ int device_cus() {
 // query-head group and still leaves about two workgroups per compute unit
 // (`rows` query rows in all); fewer for wide heads, whose per-head state (q
 // and the output accumulator) is larger. The choice only decides which loads
-// are shared.
-int heads_per_group(int64_t G, int64_t D, int64_t rows) {
-  const int cap = D <= 64 ? 8 : (D <= 128 ? 4 : 2);
+// are shared. For D = 128, four heads share one kv stream's loads (decode is
+// bandwidth-bound), but need 278 registers, one wave per SIMD; prefill (more
+// than 16 query rows) takes two, at 200 registers and twice the waves
+// (L = 2048 causal: 1.96 -> 1.38 ms).
+int heads_per_group(int64_t G, int64_t D, int64_t rows, int64_t qL) {
+  const int cap = D <= 64 ? 8 : (D <= 128 ? (qL > 16 ? 2 : 4) : 2);
   const int64_t want = 2 * (int64_t)device_cus();
   for (int gc = cap; gc > 1; gc >>= 1)
     if (G % gc == 0 && rows / gc >= want) return gc;
@@ -437,7 +440,7 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
   // fp32 runs on the VALU kernel above; bf16 and f16 on matrix cores
   // (bi_sdpa_mfma.hip). Each is the only arithmetic for its element type.
   if (dtype == BI_F32) {
-    const int gc = heads_per_group(H / Hkv, D, rows);
+    const int gc = heads_per_group(H / Hkv, D, rows, qL);
     SdpaFn fn = kernel_for_dims<float>(D, V, gc);
     hipLaunchKernelGGL(fn, dim3((unsigned)(rows / gc)), dim3(kThreads), 0,
                        static_cast<hipStream_t>(hip_stream), p);
