@@ -322,15 +322,17 @@ def test_padding_steps_change_no_bit(cuda):
             b[:, 0] = 1.0
             b[:, 1] = -0.0
             a[3, 5] = float("inf")
-            outs = {}
-            for gi in range(len(geos)):
-                try:
-                    outs[gi] = bits(_gemm._gemm(a, b, None, False, geometry=gi))
-                except NotImplementedError:
-                    continue
-            ref = outs[0]
-            for gi, o in outs.items():
-                assert (o == ref).all(), "%s K=%d geometry %s differs" % (dname, K, geos[gi])
+            for trans_b, bb in ((False, b), (True, b.t().contiguous())):
+                outs = {}
+                for gi in range(len(geos)):
+                    try:
+                        outs[gi] = bits(_gemm._gemm(a, bb, None, trans_b, geometry=gi))
+                    except NotImplementedError:
+                        continue
+                ref = outs[0]
+                for gi, o in outs.items():
+                    assert (o == ref).all(), "%s K=%d trans_b=%s geometry %s differs" % (
+                        dname, K, trans_b, geos[gi])
             y = _gemm._gemm(a, b, None, False)
             z = torch.zeros((), dtype=dtype, device=cuda)
             for r, c in [(0, 0), (0, 7), (1, 3), (2, 0), (0, 1)]:
