@@ -102,12 +102,17 @@ int bi_gemm(const void* a, const void* b, const void* bias, void* out,
  * chains are combined in a fixed order. Nothing in the reduction depends on
  * B, qL, the other query rows, or N beyond which keys exist, so growing the
  * context with masked keys leaves earlier results bitwise unchanged. A query
- * row whose keys are all masked yields 0. Values of keys that an array mask
- * hides from every query sharing a workgroup are never used, whatever they
- * hold (as in the reference, which skips masked keys); the matrix-core path
- * multiplies the values of other unused keys in a block (another query's
- * masked or future keys) by zero, so those must be finite.
- * Supported head dims: D == V in {64, 128, 256}.
+ * row whose keys are all masked yields 0. A sink enters the fixed-order
+ * combine as one more partial (m = sink, l = 1, o = 0).
+ * Keys that no query row can see -- past every row's causal bound (e.g. an
+ * unwritten cache tail) or hidden by an array mask from every query sharing a
+ * workgroup -- never reach the output, whatever they hold (the reference skips
+ * them, _attention.py:92-98). The matrix-core path multiplies the values of a
+ * key that is visible to another query row of the same 32-key block, but not
+ * to this one, by zero; a NaN or infinity there, which reaches that other
+ * row's output in any case, also reaches this row's.
+ * Supported head dims (D, V): D == V in {32, 64, 96, 128, 160, 192, 224, 256}
+ * and (192, 128); other multiples of 32 return BI_EUNSUPPORTED.
  */
 int bi_sdpa(const void* q, const void* k, const void* v,
             const void* mask, const int64_t* mask_strides,

@@ -50,6 +50,43 @@ int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
                            const void* biases, void* out, int64_t M, int64_t N, int64_t K,
                            int group_size, int bits, int dtype, int g, void* hip_stream);
 
+/*
+ * Attention launch shapes. bi_sdpa picks a launch shape from the grid alone:
+ * for BI_F16 / BI_BF16 (matrix cores) how many 16-column tiles a workgroup
+ * holds (a column is one (query head, query row) pair of a kv head) and over
+ * how many workgroups the output dims are split; for BI_F32 how many query
+ * heads share a workgroup's key and value loads. The reference has a single
+ * launch shape (reference _attention.py:241-250: one threadgroup per row);
+ * every shape here runs the same per-column arithmetic, and these entry
+ * points let a test run one input through every shape and compare bits.
+ *
+ * Shapes of BI_F16 / BI_BF16: 0 "rows" (prefill: 2 column tiles per
+ * workgroup, 1 for head dims above 128), 1 one tile, 2 / 3 / 4 one tile with
+ * the output dims split over 2 / 4 / 8 workgroups (fewer where the value
+ * head dim does not allow it). Shapes of BI_F32: s = 0..3, 2^s query heads
+ * per workgroup.
+ */
+
+/* The shape bi_sdpa picks for this problem on a GPU of `cus` compute units
+ * (0: the current device's). Returns the shape (>= 0) or a negative status. */
+int bi_sdpa_pick_shape(int64_t B, int64_t H, int64_t Hkv, int64_t qL, int64_t D, int64_t V,
+                       int dtype, int cus);
+
+/* Columns (BI_F32: query heads) and output-dim splits per workgroup of a
+ * shape; BI_EINVAL if that shape is not built for the head dims. */
+int bi_sdpa_shape_info(int64_t D, int64_t V, int dtype, int shape, int* columns, int* splits);
+
+/* bi_sdpa with the launch shape forced to `shape` (same arguments and
+ * semantics). BI_F32 shapes must divide the query heads of a kv head. */
+int bi_sdpa_with_shape(const void* q, const void* k, const void* v,
+                       const void* mask, const int64_t* mask_strides,
+                       const void* sinks, void* out,
+                       int64_t B, int64_t H, int64_t Hkv, int64_t qL, int64_t N,
+                       int64_t D, int64_t V,
+                       const int64_t* qkv_strides,
+                       float scale, int mask_mode, int64_t causal_offset,
+                       int dtype, int shape, void* hip_stream);
+
 /* Wavefront width the kernels were compiled for (64 on gfx950); the fixed
  * reduction shapes assume it. Reads a device-side constant: needs a GPU. */
 int bi_device_wavefront_size(int* out);

@@ -295,11 +295,6 @@ __global__ void __launch_bounds__(kThreads) sdpa_kernel(SdpaArgs p) {
   }
 }
 
-using SdpaFn = void (*)(SdpaArgs);
-
-// Heads per workgroup: the largest supported count that divides the
-// query-head group; fewer for wide heads, whose per-head state (q and the
-// output accumulator) is larger.
 // Compute units of the current device, read once per device.
 int device_cus() {
   static std::atomic<int> cached[64];
@@ -315,60 +310,123 @@ int device_cus() {
   return n;
 }
 
-// Heads per workgroup: the largest supported count that divides the
-// query-head group and still leaves about two workgroups per compute unit
-// (`rows` query rows in all); fewer for wide heads, whose per-head state (q
-// and the output accumulator) is larger. The choice only decides which loads
-// are shared. For D = 128, four heads share one kv stream's loads (decode is
+// ---------------------------------------------------------------- fp32 shapes
+// Shape s of the fp32 kernel groups GC = 2^s query heads per workgroup
+// (s = 0..3). The choice only decides which loads are shared.
+
+// Largest heads-per-workgroup built for the head dims: the per-head state
+// (q and the output accumulator) grows with them.
+int f32_max_group(int64_t D, int64_t V) {
+  const int64_t w = D > V ? D : V;
+  return w <= 64 ? 8 : w <= 128 ? 4 : 2;
+}
+
+// Heads per workgroup: the largest count that divides the query-head group
+// and still leaves about two workgroups per compute unit (`rows` query rows in
+// all). For D = 128, four heads share one kv stream's loads (decode is
 // bandwidth-bound), but need 278 registers, one wave per SIMD; prefill (more
 // than 16 query rows) takes two, at 200 registers and twice the waves
 // (L = 2048 causal: 1.96 -> 1.38 ms).
-int heads_per_group(int64_t G, int64_t D, int64_t rows, int64_t qL) {
-  const int cap = D <= 64 ? 8 : (D <= 128 ? (qL > 16 ? 2 : 4) : 2);
-  const int64_t want = 2 * (int64_t)device_cus();
+int f32_pick_shape(int64_t G, int64_t D, int64_t V, int64_t rows, int64_t qL, int cus) {
+  int cap = f32_max_group(D, V);
+  if (cap == 4 && qL > 16) cap = 2;
+  const int64_t want = 2 * (int64_t)cus;
+  int s = 0;
   for (int gc = cap; gc > 1; gc >>= 1)
-    if (G % gc == 0 && rows / gc >= want) return gc;
-  return 1;
+    if (G % gc == 0 && rows / gc >= want) {
+      while ((1 << s) < gc) s++;
+      return s;
+    }
+  return 0;
 }
 
-template <typename T, int D>
-SdpaFn kernel_for_group(int gc) {
+template <typename T, int D, int V>
+SdpaKernelFn f32_kernel_for_group(int gc) {
   constexpr int PF = 2;
+  constexpr int W = D > V ? D : V;
   switch (gc) {
-    case 1: return sdpa_kernel<T, D, D, 1, PF>;
-    case 2: return sdpa_kernel<T, D, D, 2, PF>;
+    case 1: return sdpa_kernel<T, D, V, 1, PF>;
+    case 2: return sdpa_kernel<T, D, V, 2, PF>;
     case 4:
-      if constexpr (D <= 128) return sdpa_kernel<T, D, D, 4, PF>;
+      if constexpr (W <= 128) return sdpa_kernel<T, D, V, 4, PF>;
       break;
     case 8:
-      if constexpr (D <= 64) return sdpa_kernel<T, D, D, 8, PF>;
+      if constexpr (W <= 64) return sdpa_kernel<T, D, V, 8, PF>;
       break;
   }
   return nullptr;
 }
 
-template <typename T>
-SdpaFn kernel_for_dims(int64_t D, int64_t V, int gc) {
-  if (D != V) return nullptr;
-  switch (D) {
-    case 64: return kernel_for_group<T, 64>(gc);
-    case 128: return kernel_for_group<T, 128>(gc);
-    case 256: return kernel_for_group<T, 256>(gc);
-  }
+SdpaKernelFn f32_kernel(int64_t D, int64_t V, int shape) {
+  if (shape < 0 || shape > 3) return nullptr;
+#define BI_F32_CASE(d, v) \
+  if (D == d && V == v) return f32_kernel_for_group<float, d, v>(1 << shape);
+  BI_SDPA_DIM_PAIRS(BI_F32_CASE)
+#undef BI_F32_CASE
   return nullptr;
 }
 
-// The head dims built for every element type (fp32 here, bf16 / f16 in
-// bi_sdpa_mfma.hip).
-bool dims_built(int64_t D, int64_t V) { return D == V && (D == 64 || D == 128 || D == 256); }
+// ---------------------------------------------------------------- MFMA shapes
 
-}  // namespace
+SdpaKernelFn mfma_kernel(int64_t D, int64_t V, int dtype, bool mask, int shape) {
+#define BI_MFMA_CASE(d, v) \
+  if (D == d && V == v) return sdpa_mfma_kernel_d##d##_v##v(dtype, mask, shape);
+  BI_SDPA_DIM_PAIRS(BI_MFMA_CASE)
+#undef BI_MFMA_CASE
+  return nullptr;
+}
 
-extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* mask,
-                       const int64_t* mask_strides, const void* sinks, void* out, int64_t B,
-                       int64_t H, int64_t Hkv, int64_t qL, int64_t N, int64_t D, int64_t V,
-                       const int64_t* qkv_strides, float scale, int mask_mode,
-                       int64_t causal_offset, int dtype, void* hip_stream) {
+// "Rows" when a kv head has more than 16 columns (prefill) and that grid fills
+// the compute units; otherwise one column tile, with the output dims split
+// over 2, 4 or 8 workgroups when the grid of column tiles would leave compute
+// units idle: decode, and short chunks of prefill such as 16 query rows.
+int mfma_pick_shape(int64_t D, int64_t V, int64_t ncol, int64_t streams, int cus) {
+  const int rc = sdpa_shape_columns(D, V, SDPA_ROWS);
+  if (ncol > 16 && streams * ((ncol + rc - 1) / rc) >= cus) return SDPA_ROWS;
+  const int64_t tiles = streams * ((ncol + 15) / 16);  // workgroups at one column tile
+  if (tiles >= cus) return SDPA_TILE;
+  if (2 * tiles >= cus) return SDPA_SPLIT2;
+  if (4 * tiles >= cus) return SDPA_SPLIT4;
+  return SDPA_SPLIT8;
+}
+
+bool dims_built(int64_t D, int64_t V) {
+#define BI_DIMS_CASE(d, v) \
+  if (D == d && V == v) return true;
+  BI_SDPA_DIM_PAIRS(BI_DIMS_CASE)
+#undef BI_DIMS_CASE
+  return false;
+}
+
+int pick_shape(int64_t B, int64_t H, int64_t Hkv, int64_t qL, int64_t D, int64_t V, int dtype,
+               int cus) {
+  if (dtype == BI_F32) return f32_pick_shape(H / Hkv, D, V, B * H * qL, qL, cus);
+  return mfma_pick_shape(D, V, (H / Hkv) * qL, B * Hkv, cus);
+}
+
+// Columns (query heads for fp32, (head, row) columns otherwise) and output-dim
+// splits per workgroup of a shape; false if it is not built.
+bool shape_geometry(int64_t D, int64_t V, int dtype, int shape, int* columns, int* splits) {
+  if (dtype == BI_F32) {
+    if (!f32_kernel(D, V, shape)) return false;
+    *columns = 1 << shape;
+    *splits = 1;
+    return true;
+  }
+  if (shape < 0 || shape >= SDPA_NUM_SHAPES || !mfma_kernel(D, V, dtype, false, shape))
+    return false;
+  *columns = sdpa_shape_columns(D, V, shape);
+  *splits = sdpa_shape_splits(V, shape);
+  return true;
+}
+
+// Validates, packs the arguments and launches shape `shape` (-1: the shape
+// bi_sdpa picks).
+int sdpa_run(const void* q, const void* k, const void* v, const void* mask,
+             const int64_t* mask_strides, const void* sinks, void* out, int64_t B, int64_t H,
+             int64_t Hkv, int64_t qL, int64_t N, int64_t D, int64_t V,
+             const int64_t* qkv_strides, float scale, int mask_mode, int64_t causal_offset,
+             int dtype, int shape, void* hip_stream) {
   const int esz = bi::elem_size(dtype);
   if (!esz) return bi::fail(BI_EINVAL, "bi_sdpa: unknown dtype %d", dtype);
   if (B < 0 || H <= 0 || Hkv <= 0 || qL < 0 || N < 0 || D <= 0 || V <= 0)
@@ -383,7 +441,8 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
     return bi::fail(BI_EINVAL, "bi_sdpa: array mask needs a mask pointer and strides");
   if (!dims_built(D, V))
     return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: head dims D=%lld V=%lld are not built "
-                    "(supported: D == V in {64, 128, 256})", (long long)D, (long long)V);
+                    "(supported: D == V in {32, 64, ..., 256}, and D = 192 with V = 128)",
+                    (long long)D, (long long)V);
   const int64_t rows = B * H * qL;
   if (rows == 0) return BI_OK;
   if (rows > INT32_MAX) return bi::fail(BI_EINVAL, "bi_sdpa: B*H*qL too large");
@@ -430,25 +489,81 @@ extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* 
   // and a batch's mask, with 32-bit byte offsets.
   if (dtype != BI_F32) {
     const int64_t st = p.ks[2] > p.vs[2] ? p.ks[2] : p.vs[2];
-    if ((32 * st + D) * esz > INT32_MAX)
+    if ((32 * st + (D > V ? D : V)) * esz > INT32_MAX)
       return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: key/value row stride %lld is too large",
                       (long long)st);
     if (mask_mode == BI_MASK_ARRAY &&
         ((H - 1) * p.ms[1] + (qL - 1) * p.ms[2] + N + kMaskSlack) * esz > INT32_MAX)
       return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: the mask of one batch entry is too large");
   }
+  if (shape < 0) shape = pick_shape(B, H, Hkv, qL, D, V, dtype, device_cus());
+  int columns = 0, splits = 0;
+  if (!shape_geometry(D, V, dtype, shape, &columns, &splits))
+    return bi::fail(BI_EINVAL, "bi_sdpa: launch shape %d is not built for dtype %d D=%lld V=%lld",
+                    shape, dtype, (long long)D, (long long)V);
   // fp32 runs on the VALU kernel above; bf16 and f16 on matrix cores
-  // (bi_sdpa_mfma.hip). Each is the only arithmetic for its element type.
+  // (bi_sdpa_mfma_kernel.h). Each is the only arithmetic for its element type.
+  SdpaKernelFn fn;
+  int64_t blocks;
   if (dtype == BI_F32) {
-    const int gc = heads_per_group(H / Hkv, D, rows, qL);
-    SdpaFn fn = kernel_for_dims<float>(D, V, gc);
-    hipLaunchKernelGGL(fn, dim3((unsigned)(rows / gc)), dim3(kThreads), 0,
-                       static_cast<hipStream_t>(hip_stream), p);
-  } else if (!sdpa_mfma_launch(p, dtype, D, device_cus(), static_cast<hipStream_t>(hip_stream))) {
-    return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: no MFMA kernel for dtype %d D=%lld", dtype,
-                    (long long)D);
+    if ((H / Hkv) % columns)
+      return bi::fail(BI_EINVAL, "bi_sdpa: %d heads per workgroup do not divide the %lld query "
+                      "heads of a kv head", columns, (long long)(H / Hkv));
+    fn = f32_kernel(D, V, shape);
+    blocks = rows / columns;
+  } else {
+    fn = mfma_kernel(D, V, dtype, mask_mode == BI_MASK_ARRAY, shape);
+    const int64_t ncol = (H / Hkv) * qL;
+    blocks = B * Hkv * ((ncol + columns - 1) / columns) * splits;
   }
+  if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_sdpa: grid too large");
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(hip_stream), p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return bi::launch_error(e, "bi_sdpa launch");
+  return BI_OK;
+}
+
+}  // namespace
+
+extern "C" int bi_sdpa(const void* q, const void* k, const void* v, const void* mask,
+                       const int64_t* mask_strides, const void* sinks, void* out, int64_t B,
+                       int64_t H, int64_t Hkv, int64_t qL, int64_t N, int64_t D, int64_t V,
+                       const int64_t* qkv_strides, float scale, int mask_mode,
+                       int64_t causal_offset, int dtype, void* hip_stream) {
+  return sdpa_run(q, k, v, mask, mask_strides, sinks, out, B, H, Hkv, qL, N, D, V, qkv_strides,
+                  scale, mask_mode, causal_offset, dtype, -1, hip_stream);
+}
+
+extern "C" int bi_sdpa_with_shape(const void* q, const void* k, const void* v, const void* mask,
+                                  const int64_t* mask_strides, const void* sinks, void* out,
+                                  int64_t B, int64_t H, int64_t Hkv, int64_t qL, int64_t N,
+                                  int64_t D, int64_t V, const int64_t* qkv_strides, float scale,
+                                  int mask_mode, int64_t causal_offset, int dtype, int shape,
+                                  void* hip_stream) {
+  if (shape < 0) return bi::fail(BI_EINVAL, "bi_sdpa_with_shape: shape %d", shape);
+  return sdpa_run(q, k, v, mask, mask_strides, sinks, out, B, H, Hkv, qL, N, D, V, qkv_strides,
+                  scale, mask_mode, causal_offset, dtype, shape, hip_stream);
+}
+
+extern "C" int bi_sdpa_pick_shape(int64_t B, int64_t H, int64_t Hkv, int64_t qL, int64_t D,
+                                  int64_t V, int dtype, int cus) {
+  if (!bi::elem_size(dtype)) return bi::fail(BI_EINVAL, "bi_sdpa_pick_shape: unknown dtype %d", dtype);
+  if (B <= 0 || H <= 0 || Hkv <= 0 || qL <= 0 || H % Hkv || cus < 0)
+    return bi::fail(BI_EINVAL, "bi_sdpa_pick_shape: bad sizes");
+  if (!dims_built(D, V))
+    return bi::fail(BI_EUNSUPPORTED, "bi_sdpa_pick_shape: head dims D=%lld V=%lld are not built",
+                    (long long)D, (long long)V);
+  return pick_shape(B, H, Hkv, qL, D, V, dtype, cus > 0 ? cus : device_cus());
+}
+
+extern "C" int bi_sdpa_shape_info(int64_t D, int64_t V, int dtype, int shape, int* columns,
+                                  int* splits) {
+  int c = 0, w = 0;
+  if (!bi::elem_size(dtype) || !shape_geometry(D, V, dtype, shape, &c, &w))
+    return bi::fail(BI_EINVAL, "bi_sdpa_shape_info: no shape %d for dtype %d D=%lld V=%lld",
+                    shape, dtype, (long long)D, (long long)V);
+  if (columns) *columns = c;
+  if (splits) *splits = w;
   return BI_OK;
 }

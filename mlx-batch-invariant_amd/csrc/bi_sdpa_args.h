@@ -1,5 +1,6 @@
-// Launch arguments shared by the attention kernels (bi_sdpa.hip, the VALU
-// kernel for fp32; bi_sdpa_mfma.hip, the MFMA kernel for bf16 and f16).
+// Launch arguments and launch shapes shared by the attention kernels
+// (bi_sdpa.hip: the VALU kernel for fp32 and the C entry points;
+// bi_sdpa_mfma_kernel.h: the MFMA kernel for bf16 and f16).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -19,8 +20,46 @@ struct SdpaArgs {
   int64_t causal_offset;
 };
 
-// Launches the MFMA attention kernel for bf16 / f16 with D == V in
-// {64, 128, 256} (bi_sdpa_mfma.hip) on a device with `cus` compute units.
-// Returns false when it is not built for the dtype and head dim (the caller
-// then uses the VALU kernel).
-bool sdpa_mfma_launch(const SdpaArgs& p, int dtype, int64_t D, int cus, hipStream_t stream);
+typedef void (*SdpaKernelFn)(SdpaArgs);
+
+// Head-dim pairs (D for queries and keys, V for values) built for every
+// element type. The reference accepts any multiples of 32
+// (mlx_batch_invariant/_attention.py:224-227); these are the ones compiled.
+#define BI_SDPA_DIM_PAIRS(X) \
+  X(32, 32) X(64, 64) X(96, 96) X(128, 128) X(160, 160) X(192, 192) X(224, 224) X(256, 256) \
+  X(192, 128)
+
+// Launch shapes of the MFMA kernel (bf16 / f16). None of them enters a
+// column's arithmetic; they decide which workgroup, wave and lane evaluate a
+// column and how operands travel.
+//   SDPA_ROWS    several 16-column tiles per workgroup (prefill)
+//   SDPA_TILE    one column tile, output dims whole (or split in two for V > 128)
+//   SDPA_SPLITn  one column tile, output dims split over n workgroups (decode),
+//                capped by the largest power of two that leaves each workgroup
+//                a multiple of 16 dims
+enum SdpaShape { SDPA_ROWS = 0, SDPA_TILE = 1, SDPA_SPLIT2 = 2, SDPA_SPLIT4 = 3, SDPA_SPLIT8 = 4,
+                 SDPA_NUM_SHAPES = 5 };
+
+// Heads wider than 128 carry more registers per column: one column tile per
+// rows workgroup, no key prefetch, value dims always split at least in two.
+constexpr bool sdpa_wide(int64_t D, int64_t V) { return D > 128 || V > 128; }
+constexpr int sdpa_rows_tiles(int64_t D, int64_t V) { return sdpa_wide(D, V) ? 1 : 2; }
+constexpr int sdpa_splits_max(int64_t V) {
+  return (V / 16) % 8 == 0 ? 8 : (V / 16) % 4 == 0 ? 4 : (V / 16) % 2 == 0 ? 2 : 1;
+}
+constexpr int sdpa_splits_min(int64_t V) { return V > 128 ? 2 : 1; }
+constexpr int sdpa_shape_splits(int64_t V, int shape) {
+  const int want = shape <= SDPA_TILE ? 1 : 1 << (shape - 1);
+  const int capped = want < sdpa_splits_max(V) ? want : sdpa_splits_max(V);
+  return capped > sdpa_splits_min(V) ? capped : sdpa_splits_min(V);
+}
+constexpr int sdpa_shape_columns(int64_t D, int64_t V, int shape) {
+  return shape == SDPA_ROWS ? 16 * sdpa_rows_tiles(D, V) : 16;
+}
+
+// The MFMA kernel of one head-dim pair for (dtype, array mask or not, shape);
+// nullptr for an element type it is not built for (bi_sdpa_mfma_d*.hip).
+#define BI_SDPA_MFMA_DECLARE(D, V) \
+  SdpaKernelFn sdpa_mfma_kernel_d##D##_v##V(int dtype, bool mask, int shape);
+BI_SDPA_DIM_PAIRS(BI_SDPA_MFMA_DECLARE)
+#undef BI_SDPA_MFMA_DECLARE

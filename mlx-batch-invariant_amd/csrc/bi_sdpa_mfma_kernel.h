@@ -1,4 +1,6 @@
-// Batch-invariant single-pass attention on MFMA (gfx950), bf16 and f16.
+// Batch-invariant single-pass attention on MFMA (gfx950), bf16 and f16: the
+// kernel template, included by one instantiation unit per built head-dim pair
+// (bi_sdpa_mfma_d*.hip); bi_sdpa_mfma.hip chooses the launch shape.
 //
 // Restates the reference bi_sdpa (mlx_batch_invariant/_attention.py:32-149)
 // with matrix cores: one workgroup owns the whole key reduction for each of
@@ -8,6 +10,8 @@
 // query length or context length. The workgroup's 4 waves walk the keys in a
 // fixed stride order (the reference's fixed per-simdgroup strides, :89) and
 // their partial results are merged in a fixed order through LDS (:124-141).
+// D is the query/key head dim and V the value head dim (both multiples of 32,
+// reference :33-34, :224-227).
 //
 // Fixed per-column arithmetic (the invariance contract):
 //   * Keys are taken in blocks of 32 (block b = keys 32b .. 32b + 31). Block b
@@ -28,15 +32,21 @@
 //     split into hi and lo = T(p - hi), hi = p truncated to bf16 (bf16) or
 //     T(p) (f16): for each 16-dim block, keys
 //     0-15 hi, keys 0-15 lo, keys 16-31 hi, keys 16-31 lo. m starts at the
-//     lowest finite float and l at 0; a sink starts chain 0 at m =
-//     sink * log2 e, l = 1 (reference :80-86).
-//   * Merge: M = max over the chains' m; for c = 0, 1, 2, 3 in order,
-//     e_c = exp2(m_c - M), L = fma(l_c, e_c, L) and O = fma(o_c, e_c, O) from
-//     L = O = +0.0; out = L == 0 ? O : O / L, one rounding to T.
+//     lowest finite float and l at 0 (reference :76-79).
+//   * Merge: a sink (reference :80-86, an extra denominator term exp(sink))
+//     enters here as one more partial with m = sink * log2 e, l = 1, o = 0,
+//     ahead of the chains: M = max of the sink's and the chains' m;
+//     L = exp2(sink2 - M) (0 without a sink), O = +0.0; then for
+//     c = 0, 1, 2, 3 in order, e_c = exp2(m_c - M), L = fma(l_c, e_c, L) and
+//     O = fma(o_c, e_c, O); out = L == 0 ? O : O / L, one rounding to T.
+//     (Seeding a chain's base with the sink, as the reference seeds its
+//     simdgroup 0, would put a large sink's p below the f16 planes' range.)
 // Every column, whatever workgroup or lane it lands in, however many rows or
 // heads share its keys and whatever the launch shape (columns per workgroup,
 // prefetch depths), runs exactly this sequence: an output row has the same
 // bits for any batch, query length and context past its visible keys.
+#pragma once
+
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <math.h>
@@ -205,16 +215,16 @@ __device__ inline float col_max(float x) { return half_pair(row_pair(x, true), t
 
 // Launch shape: CT column tiles of 16 columns per workgroup, shared by the 4
 // waves (one chain each); WS workgroups split a column tile's output dims
-// (each computes the same scores and statistics, and o for D / WS dims); a
+// (each computes the same scores and statistics, and o for V / WS dims); a
 // wave's keys are loaded PK blocks ahead into registers (or, KL, into its
 // LDS slots beside the values, by contiguous loads) and its values SV - 1
 // blocks ahead into its own LDS slots; an array mask's values (MK) are
 // loaded with the keys (MK = 1) or at the start of their own block (MK = 2,
 // one register set). None of these enters a column's arithmetic.
-template <typename T, int D, int CT, int PK, int SV, int WS, int MK, bool KL>
+template <typename T, int D, int V, int CT, int PK, int SV, int WS, int MK, bool KL>
 struct Chain {
   static constexpr int NQ = D / 32;            // score MFMAs per 16 keys
-  static constexpr int DW = D / WS;            // output dims per workgroup
+  static constexpr int DW = V / WS;            // output dims per workgroup
   static constexpr int NB = DW / 16;           // 16-dim blocks of o held
   static constexpr int VCH = DW / 8;           // 16-byte chunks per value row held
   static constexpr int CH = D / 8;             // 16-byte chunks per key row
@@ -235,7 +245,8 @@ struct Chain {
   // key blocks, which keeps the count when PK >= SV - 2).
   static constexpr int VWAIT = (SV - 1) * (NKL + DK + DV);
   static_assert(SV >= 2 && SV <= 6 && PK >= 0 && (KL ? PK == 0 && !MK : PK >= SV - 2) &&
-                    D % (16 * WS) == 0 && VCH >= 2,
+                    D % 32 == 0 && V % (16 * WS) == 0 && VCH >= 2 &&
+                    (!KL || (CH & (CH - 1)) == 0),
                 "shape");
   static_assert(VWAIT <= 63, "value loads in flight exceed the vmcnt range");
   static_assert(SV * ARR_U4 * 16 <= 160 * 1024, "LDS per workgroup");
@@ -243,19 +254,24 @@ struct Chain {
   // slot array exactly and its (m, l) fit in another.
   static_assert(kWaves * NB * 64 <= ARR_U4 && kWaves * 64 / 2 <= ARR_U4, "merge staging");
 
-  // Value slot: [32 keys][VCH chunks], chunk c of key r at c ^ swz_v(r).
-  // ds_read_tr16_b64: lane group g reads keys 4g + (0..3), 16 dims (32 bytes,
-  // a chunk pair) each; by the bank-conflict counter one pass serves groups 0
-  // and 1 (then 2 and 3), i.e. 8 consecutive keys. The LDS has 64 banks of 4
-  // bytes; with RP keys per 256 bytes, XORing key r's chunk pairs with
-  // (r / RP) mod (pairs per row, at most 8) puts those 8 keys on distinct banks.
-  __device__ __forceinline__ static int swz_v(int r) {
-    constexpr int ROWB = VCH * 16, RP = ROWB >= 256 ? 1 : 256 / ROWB;
-    constexpr int PB = ROWB / 32 < 8 ? ROWB / 32 : 8;
-    if constexpr (PB > 1)
-      return ((r / RP) & (PB - 1)) << 1;
-    else
-      return 0;
+  // Value slot: [32 keys][NPR chunk pairs], 32-byte pair j of key r stored at
+  // pair (j + rot(r)) mod NPR. ds_read_tr16_b64: lane group g reads keys
+  // 4g + (0..3), one pair (16 dims) each; by the bank-conflict counter one
+  // pass serves groups 0 and 1 (then 2 and 3), i.e. 8 consecutive keys, so
+  // those 8 pairs must fall in distinct 8-bank groups of the 64 banks of 4
+  // bytes: key r's pair lands in group (r * NPR + pair) mod 8. With 2^t the
+  // largest power of two (at most 8) dividing NPR, rot(r) = (r mod 8) >> (3 - t)
+  // separates them for every NPR (checked exhaustively for NPR = 1..16).
+  static constexpr int NPR = VCH / 2;
+  static constexpr int ROT_SHIFT = NPR % 8 == 0 ? 0 : NPR % 4 == 0 ? 1 : NPR % 2 == 0 ? 2 : 3;
+  __device__ __forceinline__ static int rot_v(int r) { return (r & 7) >> ROT_SHIFT; }
+  // LDS chunk of value chunk c of key r, and the value chunk stored at LDS
+  // chunk c of key r.
+  __device__ __forceinline__ static int vchunk_lds(int r, int c) {
+    return 2 * (((c >> 1) + rot_v(r)) % NPR) + (c & 1);
+  }
+  __device__ __forceinline__ static int vchunk_src(int r, int c) {
+    return 2 * (((c >> 1) + NPR - rot_v(r)) % NPR) + (c & 1);
   }
   // Key slot (KL): [32 keys][CH chunks], chunk c of key r at c ^ swz_k(r): the
   // score MFMAs' A reads (16 keys, one chunk each) then hit distinct banks.
@@ -278,22 +294,26 @@ struct Chain {
   uint32_t koff[2], kdoff[KL ? DK : 1], voff[DV], moff[MK ? CT : 1];
 
   // mrow: this lane's mask row offset (elements from the batch's mask) per
-  // column tile.
+  // column tile; kmax: keys that some column of the workgroup can see. The
+  // key and value streams end there, so keys no column uses (past N, or past
+  // every column's causal bound, e.g. the unwritten tail of a cache) read as
+  // zeros: their p is +0 in every column, and their values never reach o,
+  // whatever they hold (the reference never reads them, _attention.py:92-93).
   __device__ __forceinline__ void init(const SdpaArgs& p, int64_t b, int64_t kvh, int ws, int w,
-                                       int64_t n_it, int lane, const int64_t* mrow) {
+                                       int64_t n_it, int lane, const int64_t* mrow, int64_t kmax) {
     constexpr uint32_t E = sizeof(T);
     const int g = lane >> 4, r16 = lane & 15;
     kb = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
     vb = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];  // row starts
     ks2 = p.ks[2];
     vs2 = p.vs[2];
-    N = p.N;
+    N = kmax;
     nit = n_it;
     wave = w;
     if constexpr (MK) {
       // Elements of the batch's mask that any (head, row) reaches.
       mb = static_cast<const T*>(p.mask) + b * p.ms[0];
-      mext = (p.H - 1) * p.ms[1] + (p.qL - 1) * p.ms[2] + N;
+      mext = (p.H - 1) * p.ms[1] + (p.qL - 1) * p.ms[2] + p.N;
 #pragma unroll
       for (int ct = 0; ct < CT; ct++) moff[ct] = (uint32_t)((mrow[ct] + 4 * g) * E);
     }
@@ -301,7 +321,7 @@ struct Chain {
     for (int kt = 0; kt < 2; kt++) koff[kt] = (uint32_t)(((16 * kt + r16) * ks2 + 8 * g) * E);
 #pragma unroll
     for (int j = 0; j < DV; j++) {
-      const int pos = j * 64 + lane, r = pos / VCH, c = (pos % VCH) ^ swz_v(r);
+      const int pos = j * 64 + lane, r = pos / VCH, c = vchunk_src(r, pos % VCH);
       voff[j] = (uint32_t)((r * vs2 + ws * DW + c * 8) * E);
     }
     if constexpr (KL) {
@@ -312,12 +332,13 @@ struct Chain {
       }
     }
   }
-  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const T* base, int64_t stride,
+  // Rows key0 .. N - 1 of a stream whose rows hold `row` elements.
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const T* base, int64_t stride, int row,
                                                          int64_t i) const {
     const int64_t key0 = (wave + kWaves * i) * kBlk;
     const bool in = i < nit;
     return make_rsrc(base + (in ? key0 * stride : 0),
-                     in ? ((N - key0 - 1) * stride + D) * (int64_t)sizeof(T) : 0);
+                     in ? ((N - key0 - 1) * stride + row) * (int64_t)sizeof(T) : 0);
   }
   // Keys of block i into the score MFMAs' A operands: lane (r16, g) holds
   // K[16kt + r16][32q + 8g .. + 7]. Mask values: those of the lane's keys
@@ -342,7 +363,7 @@ struct Chain {
   }
   __device__ __forceinline__ void kload(int64_t i, KRegs& kr) const {
     if constexpr (!KL) {
-      const auto rs = rsrc(kb, ks2, i);
+      const auto rs = rsrc(kb, ks2, D, i);
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
 #pragma unroll
@@ -359,13 +380,13 @@ struct Chain {
     // The slot's previous reads have returned before new data lands.
     __builtin_amdgcn_s_waitcnt(kWaitLds);
     if constexpr (KL) {
-      const auto rk = rsrc(kb, ks2, i);
+      const auto rk = rsrc(kb, ks2, D, i);
 #pragma unroll
       for (int j = 0; j < DK; j++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(dst + j * 64), 16,
                                                  (int)kdoff[j], 0, 0, 0);
     }
-    const auto rs = rsrc(vb, vs2, i);
+    const auto rs = rsrc(vb, vs2, V, i);
 #pragma unroll
     for (int j = 0; j < DV; j++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + KSLOT + j * 64), 16,
@@ -373,9 +394,9 @@ struct Chain {
   }
 };
 
-template <typename T, int D, int CT, int PK, int SV, int WS, int MK, bool KL>
+template <typename T, int D, int V, int CT, int PK, int SV, int WS, int MK, bool KL>
 __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
-  using C = Chain<T, D, CT, PK, SV, WS, MK, KL>;
+  using C = Chain<T, D, V, CT, PK, SV, WS, MK, KL>;
   constexpr int NQ = C::NQ, NB = C::NB, VCH = C::VCH;
   constexpr int COLS = 16 * CT;  // columns per workgroup
   // Value slot s of every wave is array s: an LDS read then names the one
@@ -415,7 +436,8 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
     return last < 0 ? 0 : (last + 1 < p.N ? last + 1 : p.N);
   };
   const int64_t last_cc = (c0 + COLS < ncol ? c0 + COLS : ncol) - 1;
-  const int64_t nblk = (kend_of(last_cc / G) + kBlk - 1) / kBlk;
+  const int64_t kmax = kend_of(last_cc / G);  // keys some column of the workgroup sees
+  const int64_t nblk = (kmax + kBlk - 1) / kBlk;
   const int64_t kfull = kend_of(c0 / G);  // keys every column of the workgroup sees
 
   // This lane's column in each tile; its query as the B operand of the score
@@ -441,10 +463,6 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
     mrow[ct] = head[ct] * p.ms[1] + srow[ct] * p.ms[2];
     m[ct] = -FLT_MAX;
     l[ct] = 0.f;
-    if (wave == 0 && p.sinks && colv[ct]) {
-      m[ct] = (float)static_cast<const T*>(p.sinks)[head[ct]] * kLog2e;
-      l[ct] = 1.f;
-    }
 #pragma unroll
     for (int i = 0; i < NB; i++) o[ct][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
@@ -456,7 +474,7 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   const int64_t nit = nblk > wave ? (nblk - wave + kWaves - 1) / kWaves : 0;
   const int wslot = wave * C::VSLOT;  // this wave's slot within each array
   C ld;
-  ld.init(p, b, kvh, ws, wave, nit, lane, mrow);
+  ld.init(p, b, kvh, ws, wave, nit, lane, mrow, kmax);
   // One block of this chain: keys in kr, values in value slot `slot`.
   constexpr int MKCT = MK ? CT : 1;
   auto compute = [&](const typename C::KRegs& kr, const unsigned short (&mk)[MKCT][8], int slot,
@@ -584,7 +602,7 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
         // 16kt + 4g + r16 / 4 at dim col and receives V[16kt + 4g + t][16db + r16].
         const int kr = 16 * kt + 4 * g + (r16 >> 2);
         const int col = 16 * db + 4 * (r16 & 3);
-        const int chunk = (col >> 3) ^ C::swz_v(kr);
+        const int chunk = C::vchunk_lds(kr, col >> 3);
         const int off = (kr * VCH + chunk) * 16 + (col & 7) * 2;
         if constexpr (C::ASM_TR) {
           va[db][kt] = ds_read_tr((uint32_t)(uintptr_t)(lds_void_t*)vslot + off);
@@ -606,10 +624,9 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
     // are zeroed, as the reference never reads them (they may hold anything,
     // e.g. an unwritten cache slot behind a padding mask). Their p is +0 in
     // every column and o is never -0.0, so for finite values this changes no
-    // bit. Lane group g holds keys 16kt + 4g + t, t = 0..3; the ballots' 16-bit
-    // field g covers their columns. (Without a mask the only keys no column
-    // uses are past N, which load as zeros, or keys past a start-aligned causal
-    // bound, which hold real data.)
+    // bit. Lane group g holds keys 16kt + 4g + t, t = 0..3. (Without a mask,
+    // keys at or past the workgroup's last visible key read as zeros: the
+    // streams end there.)
     // OR over the 16 columns of the lane's row group (rotations by 1, 2, 4, 8
     // within each row of 16 lanes): bit 4kt + t set if some column uses key
     // 16kt + 4g + t.
@@ -687,7 +704,9 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
     __builtin_amdgcn_s_waitcnt(kWaitAll);
     asm volatile("s_barrier" ::: "memory");
     float mc[kWaves], lc[kWaves], ec[kWaves];
-    float M = -FLT_MAX;
+    // The sink (base 2) first: -FLT_MAX without one.
+    const float sk = p.sinks ? (float)static_cast<const T*>(p.sinks)[head[ct]] * kLog2e : -FLT_MAX;
+    float M = sk;
 #pragma unroll
     for (int c = 0; c < kWaves; c++) {
       const float2 v = ml[c * 64 + lane];
@@ -695,14 +714,14 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
       lc[c] = v.y;
       M = fmaxf(M, mc[c]);
     }
-    float L = 0.f;
+    float L = p.sinks ? __builtin_amdgcn_exp2f(sk - M) : 0.f;  // the sink's l = 1
 #pragma unroll
     for (int c = 0; c < kWaves; c++) {
       ec[c] = __builtin_amdgcn_exp2f(mc[c] - M);
       L = __builtin_fmaf(lc[c], ec[c], L);
     }
     T* __restrict__ out =
-        static_cast<T*>(p.out) + ((b * p.H + head[ct]) * p.qL + srow[ct]) * D + ws * C::DW;
+        static_cast<T*>(p.out) + ((b * p.H + head[ct]) * p.qL + srow[ct]) * V + ws * C::DW;
     // Wave w writes out the dim blocks w, w + 4, ... of this workgroup.
 #pragma unroll
     for (int k = 0; k < (NB + kWaves - 1) / kWaves; k++) {
@@ -725,71 +744,57 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   }
 }
 
-using Fn = void (*)(SdpaArgs);
-
-struct Shape {
-  Fn fn;
-  int cols, ws;
-};
-
-// Shapes: "rows" (two column tiles per workgroup, one for D = 256; with an
-// array mask, mask values loaded in their own block and keys not loaded ahead,
-// which keeps two workgroups per CU within the registers) when a kv head has more
-// than 16 columns (prefill) and that grid fills the compute units; otherwise
-// one column tile, with the dims split over WS workgroups when the grid of
-// column tiles would leave compute units idle (and always at least in two for
-// D = 256): decode, and short chunks of prefill such as 16 query rows. Keys
-// one block ahead and values in two slots: deeper prefetch measured no faster.
-template <typename T, int D, bool MASK>
-Shape shape_for(int64_t ncol, int64_t streams, int cus) {
-  constexpr int CT_ROWS = D == 256 ? 1 : 2;
-  constexpr int MK = MASK ? 1 : 0, MK_ROWS = MASK ? 2 : 0;
-  constexpr int PK = D == 256 ? 0 : 1;
-  constexpr int WS1 = D == 256 ? 2 : 1;  // D = 256 always splits: registers
-  constexpr int WS8 = D / 16 < 8 ? D / 16 : 8;  // at least two value chunks per row
-  // Split decode without a mask: keys through LDS by contiguous loads (three
-  // slots); with a mask or D != 128, keys in registers
-  // (measured faster for D = 128 only; D = 256 key slots would not fit LDS).
-  constexpr bool KLS = !MASK && D == 128;
-  constexpr int PKS_ = KLS ? 0 : PK, SVS_ = KLS ? 3 : 2;
-  const int64_t rows_grid = streams * ((ncol + 16 * CT_ROWS - 1) / (16 * CT_ROWS));
-  if (ncol > 16 && rows_grid >= cus)
-    return {sdpa_mfma_kernel<T, D, CT_ROWS, MASK ? 0 : PK, 2, WS1, MK_ROWS, false>, 16 * CT_ROWS,
-            WS1};
-  const int64_t tiles = streams * ((ncol + 15) / 16);  // workgroups at one column tile
-  if (tiles >= cus) return {sdpa_mfma_kernel<T, D, 1, PK, 2, WS1, MK, false>, 16, WS1};
-  if (2 * tiles >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 2, MK, KLS>, 16, 2};
-  if (4 * tiles >= cus) return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, 4, MK, KLS>, 16, 4};
-  return {sdpa_mfma_kernel<T, D, 1, PKS_, SVS_, WS8, MK, KLS>, 16, WS8};
-}
-
-template <typename T, int D>
-Shape shape_for_mask(bool mask, int64_t ncol, int64_t streams, int cus) {
-  return mask ? shape_for<T, D, true>(ncol, streams, cus) : shape_for<T, D, false>(ncol, streams, cus);
-}
-
-template <typename T>
-Shape shape_for_dims(int64_t D, bool mask, int64_t ncol, int64_t streams, int cus) {
-  switch (D) {
-    case 64: return shape_for_mask<T, 64>(mask, ncol, streams, cus);
-    case 128: return shape_for_mask<T, 128>(mask, ncol, streams, cus);
-    case 256: return shape_for_mask<T, 256>(mask, ncol, streams, cus);
+// Kernel of launch shape `SHAPE` (SdpaShape) for head dims (D, V). The rows
+// shape with an array mask loads the mask values at the start of their own
+// block and no keys ahead, which keeps two workgroups per CU within the
+// registers; the split shapes without a mask at D = V = 128 load the keys
+// through LDS by contiguous loads (three slots). Wide heads (D or V above
+// 128) load no keys ahead. Keys one block ahead and values in two slots
+// otherwise: deeper prefetch measured no faster.
+template <typename T, int D, int V, bool MASK, int SHAPE>
+constexpr SdpaKernelFn mfma_kernel() {
+  constexpr int MK = MASK ? 1 : 0;
+  constexpr int PK = sdpa_wide(D, V) ? 0 : 1;
+  constexpr int WS = sdpa_shape_splits(V, SHAPE);
+  if constexpr (SHAPE == SDPA_ROWS) {
+    return sdpa_mfma_kernel<T, D, V, sdpa_rows_tiles(D, V), MASK ? 0 : PK, 2, WS, MASK ? 2 : 0,
+                            false>;
+  } else if constexpr (SHAPE == SDPA_TILE) {
+    return sdpa_mfma_kernel<T, D, V, 1, PK, 2, WS, MK, false>;
+  } else {
+    constexpr bool KLS = !MASK && D == 128 && V == 128;
+    return sdpa_mfma_kernel<T, D, V, 1, KLS ? 0 : PK, KLS ? 3 : 2, WS, MK, KLS>;
   }
-  return {nullptr, 0, 0};
+}
+
+template <typename T, int D, int V, bool MASK>
+SdpaKernelFn mfma_kernel_shape(int shape) {
+  switch (shape) {
+    case SDPA_ROWS: return mfma_kernel<T, D, V, MASK, SDPA_ROWS>();
+    case SDPA_TILE: return mfma_kernel<T, D, V, MASK, SDPA_TILE>();
+    case SDPA_SPLIT2: return mfma_kernel<T, D, V, MASK, SDPA_SPLIT2>();
+    case SDPA_SPLIT4: return mfma_kernel<T, D, V, MASK, SDPA_SPLIT4>();
+    case SDPA_SPLIT8: return mfma_kernel<T, D, V, MASK, SDPA_SPLIT8>();
+  }
+  return nullptr;
+}
+
+template <int D, int V>
+SdpaKernelFn mfma_kernel_for(int dtype, bool mask, int shape) {
+  if (dtype == BI_BF16)
+    return mask ? mfma_kernel_shape<__bf16, D, V, true>(shape)
+                : mfma_kernel_shape<__bf16, D, V, false>(shape);
+  if (dtype == BI_F16)
+    return mask ? mfma_kernel_shape<_Float16, D, V, true>(shape)
+                : mfma_kernel_shape<_Float16, D, V, false>(shape);
+  return nullptr;
 }
 
 }  // namespace
 
-bool sdpa_mfma_launch(const SdpaArgs& p, int dtype, int64_t D, int cus, hipStream_t stream) {
-  const int64_t ncol = (p.H / p.Hkv) * p.qL;
-  const int64_t streams = p.B * p.Hkv;
-  const bool mask = p.mask_mode == BI_MASK_ARRAY;
-  const Shape sh = dtype == BI_BF16 ? shape_for_dims<__bf16>(D, mask, ncol, streams, cus)
-                 : dtype == BI_F16  ? shape_for_dims<_Float16>(D, mask, ncol, streams, cus)
-                                    : Shape{nullptr, 0, 0};
-  if (!sh.fn) return false;
-  const int64_t ncb = (ncol + sh.cols - 1) / sh.cols;
-  const int64_t blocks = streams * ncb * sh.ws;
-  hipLaunchKernelGGL(sh.fn, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
-  return true;
-}
+// Defines the lookup of one head-dim pair's kernels (declared in
+// bi_sdpa_args.h); each instantiation unit expands it once.
+#define BI_SDPA_MFMA_DEFINE(D, V)                                                   \
+  SdpaKernelFn sdpa_mfma_kernel_d##D##_v##V(int dtype, bool mask, int shape) {      \
+    return mfma_kernel_for<D, V>(dtype, mask, shape);                               \
+  }

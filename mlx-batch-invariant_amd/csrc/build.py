@@ -19,8 +19,11 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(PKG_ROOT, "_build")
 LIB = os.path.join(PKG_ROOT, "mlx_batch_invariant", "libbi.so")
 
+# Attention: one instantiation unit per built head-dim pair (BI_SDPA_DIM_PAIRS).
+SDPA_MFMA_UNITS = sorted(f for f in os.listdir(HERE)
+                         if f.startswith("bi_sdpa_mfma_d") and f.endswith(".hip"))
 SOURCES = ["bi_abi.cpp", "bi_gemm.hip", "bi_gemm_f32.hip", "bi_gemm_f16.hip", "bi_gemm_bf16.hip",
-           "bi_qgemm_f16.hip", "bi_qgemm_bf16.hip", "bi_sdpa.hip", "bi_sdpa_mfma.hip"]
+           "bi_qgemm_f16.hip", "bi_qgemm_bf16.hip", "bi_sdpa.hip", *SDPA_MFMA_UNITS]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -43,7 +46,7 @@ DEVICE_FLAGS = [
 EXTRA_FLAGS = {
     "bi_qgemm_f16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "bi_qgemm_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-    "bi_sdpa_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    **{u: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for u in SDPA_MFMA_UNITS},
 }
 
 
@@ -63,7 +66,7 @@ def _compile(src):
 
 def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 8)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
     # --no-undefined: a kernel whose host stub was not emitted fails here, not

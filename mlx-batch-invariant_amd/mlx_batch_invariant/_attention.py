@@ -1,14 +1,16 @@
 """Batch-invariant single-pass scaled dot product attention.
 
 Mirrors reference mlx_batch_invariant/_attention.py:173-250 (mask
-normalisation, validation, sinks, launch) on top of the HIP kernel in
-csrc/bi_sdpa.hip, reached through the C ABI ``bi_sdpa`` (include/bi.h).
+normalisation, validation, sinks, launch) on top of the HIP kernels in
+csrc/ (bi_sdpa.hip: fp32 on the vector ALUs; bi_sdpa_mfma_kernel.h: bf16 and
+f16 on matrix cores), reached through the C ABI ``bi_sdpa`` (include/bi.h).
 
-One workgroup owns one (batch, head, query row) and the entire reduction over
-the keys, split into 32 partial online softmaxes by key index (key i belongs to
-partial i mod 32) and combined in a fixed order. Nothing in that order depends
-on the number of query rows, the batch, or how far the key sequence extends
-past the keys a row can see.
+One workgroup owns the entire reduction over the keys for each of its query
+rows. fp32 splits it into 32 partial online softmaxes by key index (key i
+belongs to partial i mod 32); bf16/f16 into 4 chains of 32-key blocks (block b
+belongs to chain b mod 4); the partials are combined in a fixed order. Nothing
+in that order depends on the number of query rows, the batch, or how far the
+key sequence extends past the keys a row can see.
 """
 
 import math
@@ -19,14 +21,17 @@ from . import _lib
 
 PARTIALS = 32     # partial softmaxes per row = stride over the key sequence
 GROUP_LANES = 8   # lanes that share one key's dot product
-HEAD_DIMS = (64, 128, 256)  # built (D == V) head dimensions
+# Built (D, V) head-dim pairs: D for queries and keys, V for values
+# (csrc/bi_sdpa_args.h BI_SDPA_DIM_PAIRS).
+HEAD_DIMS = ((32, 32), (64, 64), (96, 96), (128, 128), (160, 160), (192, 192), (224, 224),
+             (256, 256), (192, 128))
 HEAD_DIM_MULTIPLE = 32      # the reference's own requirement (_attention.py:224-227)
 
 _SUPPORTED = (torch.float32, torch.float16, torch.bfloat16)
 
 
 def supported_head_dims(D, V):
-    return D == V and D in HEAD_DIMS
+    return (D, V) in HEAD_DIMS
 
 
 def _mask_args(mask, B, H, qL, N, dtype):
@@ -84,7 +89,9 @@ def _sdpa(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks):
     return _sdpa_eager(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks)
 
 
-def _sdpa_eager(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks):
+def _sdpa_eager(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks, shape=None):
+    """The launch; `shape` forces a launch shape (bi_sdpa_with_shape,
+    include/bi_testing.h) instead of the one bi_sdpa picks."""
     B, H, qL, D = q.shape
     _, Hkv, N, _ = k.shape
     V = v.shape[-1]
@@ -102,14 +109,29 @@ def _sdpa_eager(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks)
             B, H, Hkv, qL, N, D, V, strides, float(scale), int(mask_mode),
             int(causal_offset), _lib.DTYPE_CODES[q.dtype])
     stream, switch = _lib.launch_stream(q.device)
+    if shape is None:
+        fn, tail = L.bi_sdpa, (stream,)
+    else:
+        fn, tail = L.bi_sdpa_with_shape, (int(shape), stream)
     if switch:
         with torch.cuda.device(q.device):
-            rc = L.bi_sdpa(*args, stream)
+            rc = fn(*args, *tail)
     else:
-        rc = L.bi_sdpa(*args, stream)
+        rc = fn(*args, *tail)
     if rc:
         _lib.check(rc, "bi_sdpa")
     return out
+
+
+def launch_shape(q, k, v):
+    """The launch shape bi_sdpa picks for these operands (include/bi_testing.h):
+    _lib.SDPA_ROWS ... for bf16/f16, log2(query heads per workgroup) for fp32."""
+    B, H, qL, D = q.shape
+    L = _lib.lib()
+    rc = L.bi_sdpa_pick_shape(B, H, k.shape[1], qL, D, v.shape[-1], _lib.DTYPE_CODES[q.dtype], 0)
+    if rc < 0:
+        _lib.check(rc, "bi_sdpa_pick_shape")
+    return rc
 
 
 def scaled_dot_product_attention(q, k, v, *, scale=None, mask=None, sinks=None):
@@ -140,7 +162,7 @@ def scaled_dot_product_attention(q, k, v, *, scale=None, mask=None, sinks=None):
         raise ValueError("head dimensions must be multiples of %d, got D=%d V=%d"
                          % (HEAD_DIM_MULTIPLE, D, V))
     if not supported_head_dims(D, V):
-        raise NotImplementedError("head dimensions D=%d V=%d are not built (D == V in %s)"
+        raise NotImplementedError("head dimensions D=%d V=%d are not built (built (D, V): %s)"
                                   % (D, V, HEAD_DIMS))
 
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)

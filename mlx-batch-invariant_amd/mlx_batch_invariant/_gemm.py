@@ -17,12 +17,20 @@ from . import _lib
 
 # Fixed per-element arithmetic of the kernel. The reference exports its single
 # tile (BM, BN, BK, SG_M, SG_N) as TILE (reference _gemm.py:25-27) and a test
-# pins it; this build pins the parts that decide an element's bits: the MFMA
-# shape, the K chunk each chunk-step consumes, the fp32 chain rule and the
-# epilogue. Workgroup footprints (and the K bytes each footprint stages per
-# pipeline step) are listed separately by geometries(); they do not enter any
-# element's arithmetic.
+# pins it (reference tests/test_invariance.py:468-470). This build keeps those
+# keys for the unit of fixed arithmetic -- one wave's 16 x 16 MFMA output tile
+# (BM x BN), fed BK = 32 elements of K per chunk-step for bf16/f16 (fp32: 16,
+# K_CHUNK_FP32), by one wave (SG_M x SG_N = 1 x 1) -- and pins the rest of what
+# decides an element's bits: the MFMA instructions, the fp32 chain rule and the
+# epilogue. Workgroup footprints (how many such units a workgroup holds, and
+# the K bytes each footprint stages per pipeline step) are listed separately by
+# geometries(); they do not enter any element's arithmetic.
 TILE = dict(
+    BM=16,                               # rows of the fixed unit (one MFMA tile)
+    BN=16,                               # columns of the fixed unit
+    BK=32,                               # K per chunk-step, bf16 / f16
+    SG_M=1,                              # waves per unit, along M
+    SG_N=1,                              # waves per unit, along N
     MFMA_16BIT="v_mfma_f32_16x16x32",   # bf16 / f16 inputs, fp32 accumulate
     MFMA_FP32="v_mfma_f32_16x16x4_f32",
     K_CHUNK_16BIT=32,                    # K per MFMA for 16-bit inputs

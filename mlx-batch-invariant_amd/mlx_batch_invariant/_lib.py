@@ -48,8 +48,18 @@ SIGNATURES = {
                           _c_int, _c_int, _c_vp]),
     "bi_qgemm_with_geometry": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                         _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp]),
+    "bi_sdpa_pick_shape": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+                                    _c_int]),
+    "bi_sdpa_shape_info": (_c_int, [_c_i64, _c_i64, _c_int, _c_int, ctypes.POINTER(_c_int),
+                                    ctypes.POINTER(_c_int)]),
+    "bi_sdpa_with_shape": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64p, _c_vp, _c_vp,
+                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                    _c_i64p, _c_float, _c_int, _c_i64, _c_int, _c_int, _c_vp]),
     "bi_device_wavefront_size": (_c_int, [ctypes.POINTER(_c_int)]),
 }
+
+# Attention launch shapes (include/bi_testing.h): bf16 / f16 on matrix cores.
+SDPA_ROWS, SDPA_TILE, SDPA_SPLIT2, SDPA_SPLIT4, SDPA_SPLIT8 = 0, 1, 2, 3, 4
 
 ABI_VERSION = 1
 

@@ -124,12 +124,12 @@ def test_causal_and_masks_are_invariant(cuda):
 def test_masked_decode_is_batch_invariant(cuda):
     """An additive and a boolean mask per batch entry: a sequence's row has the
     same bits alone and at batch sizes whose grids take every launch shape
-    (dims split over 8, 4, 2 workgroups and unsplit)."""
+    (bf16/f16: dims split over 8, 4, 2 workgroups and unsplit; fp32: one, two
+    and four query heads per workgroup, whose mask rows sit at offsets of the
+    head stride)."""
     H, Hkv, N, D = 32, 8, 1000, 128
     g = torch.Generator().manual_seed(36)
     for dname, dtype in DTYPES:
-        if dtype == torch.float32:
-            continue
         q1, k1, v1 = (rn((1, H, 1, D), dtype, 37, device=cuda), rn((1, Hkv, N, D), dtype, 38, device=cuda),
                       rn((1, Hkv, N, D), dtype, 39, device=cuda))
         qp, kp, vp = (rn((64, H, 1, D), dtype, 40, device=cuda), rn((64, Hkv, N, D), dtype, 41, device=cuda),

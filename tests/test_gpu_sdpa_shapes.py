@@ -1,0 +1,292 @@
+"""GPU parity tests of the attention launch shapes and head dims.
+
+bi_sdpa picks a launch shape from the grid (include/bi_testing.h): for
+bf16/f16 the prefill "rows" shape (several 16-column tiles per workgroup), one
+tile, or one tile with the output dims split over 2/4/8 workgroups; for fp32
+how many query heads share a workgroup's loads. The reference has a single
+launch shape (_attention.py:241-250) and rejects any route switch on query
+length (reference ROADMAP.md:91-94), so every shape must give the same bits:
+
+  * every shape, forced through bi_sdpa_with_shape, gives identical bits on the
+    same input, for every built (D, V) pair, element type and mask mode;
+  * the prefill rows shape, selected by bi_sdpa itself at the shapes it is
+    built for, gives each row the bits of that row computed alone at query
+    length 1 over its visible keys (a one-tile shape), and is accurate against
+    the float64 oracle (reference tests/test_invariance.py:408-432);
+  * keys no query row can see (an unwritten cache tail) never reach the
+    output, whatever they hold (reference _attention.py:92-98).
+"""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from mlx_batch_invariant import _attention, _lib
+from oracle import sdpa as osdpa
+
+from helpers import bits, f64, rn
+
+pytestmark = pytest.mark.gpu
+
+LOW = [("float16", torch.float16), ("bfloat16", torch.bfloat16)]
+TOL = {"float32": 2e-6, "float16": 5e-3, "bfloat16": 3e-2}
+PAIRS = list(_attention.HEAD_DIMS)
+
+
+def _mask_mode(spec, q, k):
+    """(mode, mask, strides, causal_offset) for a mask spec: None, "end"
+    (bi mask="causal": row s sees keys i <= N - qL + s), "start" (torch
+    is_causal: i <= s) or an additive / boolean tensor."""
+    B, H, qL, _ = q.shape
+    N = k.shape[2]
+    if spec is None:
+        return _lib.MASK_NONE, None, (0, 0, 0), 0
+    if isinstance(spec, str):
+        return _lib.MASK_CAUSAL, None, (0, 0, 0), (N - qL if spec == "end" else 0)
+    m, ms, mode = _attention._mask_args(spec, B, H, qL, N, q.dtype)
+    return mode, m, ms, 0
+
+
+def run(q, k, v, spec=None, shape=None, sinks=None):
+    mode, m, ms, off = _mask_mode(spec, q, k)
+    return _attention._sdpa_eager(q, k, v, 1.0 / math.sqrt(q.shape[-1]), mode, m, ms, off, sinks,
+                                  shape)
+
+
+def shapes_for(dtype, D, V, G):
+    """Launch shapes built for the head dims (fp32: those dividing G heads)."""
+    L = _lib.lib()
+    code = _lib.DTYPE_CODES[dtype]
+    out = []
+    for s in range(5):
+        c, w = ctypes.c_int(), ctypes.c_int()
+        if L.bi_sdpa_shape_info(D, V, code, s, c, w) != _lib.OK:
+            continue
+        if dtype == torch.float32 and G % c.value:
+            continue
+        out.append(s)
+    return out
+
+
+def _masks(B, qL, N, dtype, device, seed):
+    g = torch.Generator().manual_seed(seed)
+    add = (torch.randn(B, 1, qL, N, generator=g)).to(dtype)
+    add[torch.rand(B, 1, qL, N, generator=g) < 0.1] = -float("inf")
+    keep = torch.rand(1, 1, qL, N, generator=g) > 0.2
+    keep[..., N - max(1, N // 10):] = False  # a padding tail
+    return add.to(device), keep.to(device)
+
+
+@pytest.mark.parametrize("D,V", PAIRS)
+def test_every_shape_gives_the_same_bits(cuda, D, V):
+    """One input through every launch shape, for each element type and mask
+    mode: the bits must not move (the attention analogue of the GEMM's
+    test_all_geometries_agree)."""
+    B, H, Hkv, qL, N = 2, 16, 2, 40, 300
+    for dname, dtype in LOW + [("float32", torch.float32)]:
+        q = rn((B, H, qL, D), dtype, 101, device=cuda)
+        k = rn((B, Hkv, N, D), dtype, 102, device=cuda)
+        v = rn((B, Hkv, N, V), dtype, 103, device=cuda)
+        sinks = rn((H,), dtype, 104, device=cuda)
+        add, keep = _masks(B, qL, N, dtype, cuda, 105)
+        shapes = shapes_for(dtype, D, V, H // Hkv)
+        assert len(shapes) >= (2 if dtype == torch.float32 else 3), shapes
+        for label, spec, sk in (("none", None, None), ("end", "end", None),
+                                ("start", "start", None), ("additive", add, None),
+                                ("bool", keep, None), ("sinks", None, sinks)):
+            ref = None
+            for s in shapes:
+                y = run(q, k, v, spec, shape=s, sinks=sk)
+                got = bits(y)
+                if ref is None:
+                    ref = got
+                    assert torch.isfinite(y).all() and bool((y != 0).any())
+                else:
+                    d = int((got != ref).sum())
+                    assert d == 0, "%s D=%d V=%d %s shape %d: %d differ" % (
+                        dname, D, V, label, s, d)
+
+
+def _oracle_rows(q, k, v, spec, rows, b, dname):
+    """float64 and reference-order fp32 results for query rows `rows` of batch
+    entry b (every head), each row as a one-row problem."""
+    B, H, qL, D = q.shape
+    N = k.shape[2]
+    qh, kh, vh = f64(q[b:b + 1]), f64(k[b:b + 1]), f64(v[b:b + 1])
+    want, fixed = [], []
+    for s in rows:
+        qs = qh[:, :, s:s + 1]
+        mask, off = None, None
+        if isinstance(spec, str):
+            off = s + (N - qL if spec == "end" else 0)
+        elif spec is not None:
+            m = spec
+            if m.dtype == torch.bool:
+                m = torch.where(m, 0.0, -float("inf"))
+            m = f64(m)
+            mask = m[(0 if m.shape[0] == 1 else b):][:1, :, (s if m.shape[2] > 1 else 0):][:, :, :1]
+        want.append(osdpa.sdpa_f64(qs, kh, vh, mask=mask, causal_offset=off))
+        fixed.append(osdpa.sdpa_fixed32(qs, kh, vh, mask=mask, causal_offset=off,
+                                        out_dtype=dname))
+    return np.concatenate(want, axis=2), np.concatenate(fixed, axis=2)
+
+
+def _alone(q, k, v, spec, b, s):
+    """Row s of batch entry b computed alone at query length 1 over the keys it
+    can see: causal rows as an unmasked call over their visible prefix, masked
+    rows with their own mask row."""
+    qL, N = q.shape[2], k.shape[2]
+    qs = q[b:b + 1, :, s:s + 1].contiguous()
+    if isinstance(spec, str):
+        nvis = min(N, s + (N - qL if spec == "end" else 0) + 1)
+        return run(qs, k[b:b + 1, :, :nvis], v[b:b + 1, :, :nvis])
+    m = spec[(0 if spec.shape[0] == 1 else b):][:1, :, (s if spec.shape[2] > 1 else 0):][:, :, :1]
+    return run(qs, k[b:b + 1], v[b:b + 1], m)
+
+
+ROWS_CASES = [(4, 64), (1, 513), (2, 513), (1, 2048), (2, 2048)]
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("dname,dtype", LOW)
+def test_prefill_rows_shape_is_invariant_and_accurate(cuda, dname, dtype, D):
+    """The prefill "rows" shape at 32/8 heads: bi_sdpa selects it for these
+    problems; rows 0, middle and last are bitwise equal to the same row computed
+    alone at query length 1 (which takes a one-tile shape), and every head of
+    those rows is within the reference's float64 bound and no worse than 4x the
+    reference-order fp32 restatement (tests:408-432). Masks: end-aligned
+    causal (mask="causal"), start-aligned causal (torch is_causal), additive
+    per row, boolean per row."""
+    H, Hkv = 32, 8
+    for B, qL in ROWS_CASES:
+        for N in (qL, 4200):
+            seed = 1000 * B + qL + N + D
+            q = rn((B, H, qL, D), dtype, seed, device=cuda)
+            k = rn((B, Hkv, N, D), dtype, seed + 1, device=cuda)
+            v = rn((B, Hkv, N, D), dtype, seed + 2, device=cuda)
+            assert _attention.launch_shape(q, k, v) == _lib.SDPA_ROWS, (B, qL, D)
+            add, keep = _masks(B, qL, N, dtype, cuda, seed + 3)
+            rows = sorted({0, qL // 2, qL - 1})
+            b = B - 1
+            for label, spec in (("end", "end"), ("start", "start"), ("additive", add),
+                                ("bool", keep)):
+                y = run(q, k, v, spec)
+                case = "%s D=%d B=%d qL=%d N=%d %s" % (dname, D, B, qL, N, label)
+                assert torch.isfinite(y).all(), case
+                for s in rows:
+                    alone = _alone(q, k, v, spec, b, s)
+                    assert np.array_equal(bits(alone[0, :, 0]), bits(y[b, :, s])), (case, s)
+                ours = f64(y[b:b + 1, :, rows])
+                want, fixed = _oracle_rows(q, k, v, spec, rows, b, dname)
+                scale = max(np.abs(want).max(), 1e-30)
+                err = np.abs(ours - want).max() / scale
+                err_fixed = np.abs(fixed - want).max() / scale
+                assert err < TOL[dname], "%s: %.3e" % (case, err)
+                assert err < 4 * err_fixed + 1e-7, "%s: %.3e vs %.3e" % (case, err, err_fixed)
+
+
+@pytest.mark.parametrize("dname,dtype", LOW + [("float32", torch.float32)])
+def test_unwritten_cache_tail_never_reaches_the_output(cuda, dname, dtype):
+    """Keys past every row's causal horizon hold NaN (an unwritten cache tail):
+    the output is finite and bitwise equal to the same call with a zero tail,
+    for start-aligned causal (torch is_causal over a longer cache) and for a
+    cache view k[:, :, :N] whose storage continues with NaN rows (mask="causal",
+    aligned to the end of the view), at decode and prefill shapes."""
+    H, Hkv, D, NP = 32, 8, 128, 1200
+    for B, qL in ((1, 1), (3, 5), (1, 300), (2, 700)):
+        q = rn((B, H, qL, D), dtype, 111, device=cuda)
+        k = rn((B, Hkv, NP, D), dtype, 112, device=cuda)
+        v = rn((B, Hkv, NP, D), dtype, 113, device=cuda)
+        # Start-aligned: row s sees keys 0..s; keys from qL on are never read.
+        kn, vn, kz, vz = k.clone(), v.clone(), k.clone(), v.clone()
+        kn[:, :, qL:] = float("nan")
+        vn[:, :, qL:] = float("nan")
+        kz[:, :, qL:] = 0
+        vz[:, :, qL:] = 0
+        got, want = run(q, kn, vn, "start"), run(q, kz, vz, "start")
+        assert torch.isfinite(got).all(), (dname, B, qL)
+        assert np.array_equal(bits(got), bits(want)), (dname, B, qL)
+        # End-aligned over a view of the first N rows; storage past N is NaN.
+        N = NP - 77
+        kn, vn, kz, vz = k.clone(), v.clone(), k.clone(), v.clone()
+        kn[:, :, N:] = float("nan")
+        vn[:, :, N:] = float("nan")
+        kz[:, :, N:] = 0
+        vz[:, :, N:] = 0
+        got = run(q, kn[:, :, :N], vn[:, :, :N], "end")
+        want = run(q, kz[:, :, :N], vz[:, :, :N], "end")
+        assert torch.isfinite(got).all(), (dname, B, qL)
+        assert np.array_equal(bits(got), bits(want)), (dname, B, qL)
+
+
+@pytest.mark.parametrize("D,V", PAIRS)
+def test_head_dims_accuracy_and_query_length_invariance(cuda, D, V):
+    """Every built (D, V) pair (the reference takes any multiples of 32,
+    _attention.py:224-227): accurate against float64 within the reference's
+    bounds, and a query row keeps its bits for query lengths 1..17."""
+    H, Hkv, N = 8, 2, 777
+    for dname, dtype in LOW + [("float32", torch.float32)]:
+        k = rn((1, Hkv, N, D), dtype, 121, device=cuda)
+        v = rn((1, Hkv, N, V), dtype, 122, device=cuda)
+        qf = rn((1, H, 17, D), dtype, 123, device=cuda)
+        base = None
+        for qL in (1, 2, 9, 16, 17):
+            q = qf[:, :, 17 - qL:].contiguous()
+            y = run(q, k, v, "end")
+            got = bits(y[:, :, -1])
+            if base is None:
+                base = got
+            else:
+                assert np.array_equal(got, base), (dname, D, V, qL)
+        want = osdpa.sdpa_f64(f64(qf), f64(k), f64(v), causal_offset=N - 17)
+        fixed = osdpa.sdpa_fixed32(f64(qf), f64(k), f64(v), causal_offset=N - 17,
+                                   out_dtype=dname)
+        err = np.abs(f64(y) - want).max() / np.abs(want).max()
+        err_fixed = np.abs(fixed - want).max() / np.abs(want).max()
+        assert err < TOL[dname], (dname, D, V, err)
+        assert err < 4 * err_fixed + 1e-7, (dname, D, V, err, err_fixed)
+
+
+def test_large_sinks_stay_accurate(cuda):
+    """A sink far above every score (up to 12 in natural-log units, where e^-12
+    is below f16's smallest normal) must not push the keys' probabilities out
+    of the half-precision planes that carry them into the value products: the
+    sink enters the fixed-order merge as its own partial, so f16 and bf16 stay
+    within the reference's bounds and within 4x the reference-order fp32
+    restatement rounded once."""
+    H, Hkv, N, D = 8, 2, 500, 128
+    for dname, dtype in LOW + [("float32", torch.float32)]:
+        q = rn((1, H, 3, D), dtype, 131, std=0.3, device=cuda)
+        k = rn((1, Hkv, N, D), dtype, 132, std=0.3, device=cuda)
+        v = rn((1, Hkv, N, D), dtype, 133, device=cuda)
+        for level in (4.0, 8.0, 12.0):
+            sinks = torch.full((H,), level, dtype=dtype, device=cuda)
+            y = run(q, k, v, None, sinks=sinks)
+            want = osdpa.sdpa_f64(f64(q), f64(k), f64(v), sinks=f64(sinks))
+            fixed = osdpa.sdpa_fixed32(f64(q), f64(k), f64(v), sinks=f64(sinks),
+                                       out_dtype=dname)
+            err = np.abs(f64(y) - want).max() / np.abs(want).max()
+            err_fixed = np.abs(fixed - want).max() / np.abs(want).max()
+            assert err < TOL[dname], (dname, level, err)
+            assert err < 4 * err_fixed + 1e-7, (dname, level, err, err_fixed)
+
+
+def test_fp32_head_grouping_prefill(cuda):
+    """fp32 groups two query heads per workgroup for prefill (more than 16 query
+    rows) and four for decode; with causal and additive masks each row keeps
+    the bits of the same row computed alone at query length 1."""
+    H, Hkv, qL, N, D = 32, 8, 64, 900, 128
+    dtype = torch.float32
+    q = rn((1, H, qL, D), dtype, 141, device=cuda)
+    k = rn((1, Hkv, N, D), dtype, 142, device=cuda)
+    v = rn((1, Hkv, N, D), dtype, 143, device=cuda)
+    add, keep = _masks(1, qL, N, dtype, cuda, 144)
+    assert _attention.launch_shape(q, k, v) == 1  # two heads per workgroup
+    for spec in ("end", "start", add, keep):
+        y = run(q, k, v, spec)
+        for s in (0, 17, qL - 1):
+            alone = _alone(q, k, v, spec, 0, s)
+            assert np.array_equal(bits(alone[0, :, 0]), bits(y[0, :, s])), s

@@ -103,11 +103,72 @@ def test_sdpa_abi_rejects_bad_arguments_without_a_gpu():
     assert call(H=6, Hkv=4) == _lib.EINVAL and "multiple" in _err()
     assert call(D=48, V=48) == _lib.EUNSUPPORTED and "head dims" in _err()
     assert call(D=128, V=64) == _lib.EUNSUPPORTED
+    assert call(D=288, V=288) == _lib.EUNSUPPORTED
     assert call(mode=5) == _lib.EINVAL
     assert call(mode=2) == _lib.EINVAL and "mask" in _err()
     assert call(dtype=9) == _lib.EINVAL
     assert call(Hkv=0) == _lib.EINVAL
     assert call(B=0) == _lib.OK and call(qL=0) == _lib.OK
+
+
+def test_sdpa_shape_abi_without_a_gpu():
+    """Shape introspection and forcing: unknown shapes are rejected before any
+    HIP call; the shape table matches the documented geometry."""
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+
+    def forced(shape, dtype=_lib.BF16, D=128, V=128, H=8, Hkv=2):
+        return L.bi_sdpa_with_shape(p, p, p, None, None, None, p, 1, H, Hkv, 1, 16, D, V, None,
+                                    0.1, 0, 0, dtype, shape, None)
+
+    assert forced(-1) == _lib.EINVAL
+    assert forced(5) == _lib.EINVAL and "shape" in _err()
+    assert forced(3, dtype=_lib.F32) == _lib.EINVAL      # 8 heads per workgroup: D <= 64 only
+    assert forced(2, dtype=_lib.F32, H=8, Hkv=4) == _lib.EINVAL  # 4 heads do not divide 2
+    assert forced(0, D=96, V=64) == _lib.EUNSUPPORTED
+
+    def info(D, V, shape, dtype=_lib.BF16):
+        c, w = ctypes.c_int(), ctypes.c_int()
+        rc = L.bi_sdpa_shape_info(D, V, dtype, shape, ctypes.byref(c), ctypes.byref(w))
+        return (c.value, w.value) if rc == _lib.OK else rc
+
+    assert info(128, 128, _lib.SDPA_ROWS) == (32, 1)
+    assert info(128, 128, _lib.SDPA_TILE) == (16, 1)
+    assert info(128, 128, _lib.SDPA_SPLIT8) == (16, 8)
+    assert info(64, 64, _lib.SDPA_SPLIT8) == (16, 4)     # at least 16 dims per workgroup
+    assert info(256, 256, _lib.SDPA_ROWS) == (16, 2)     # wide heads: one tile, dims split
+    assert info(192, 128, _lib.SDPA_ROWS) == (16, 1)
+    assert info(96, 96, _lib.SDPA_SPLIT8) == (16, 2)     # 96 = 6 x 16 dims: splits in two
+    assert info(192, 192, _lib.SDPA_SPLIT8) == (16, 4)
+    assert info(32, 32, _lib.SDPA_SPLIT4) == (16, 2)
+    assert info(128, 128, 5) == _lib.EINVAL
+    assert info(64, 64, 3, _lib.F32) == (8, 1)
+    assert info(128, 128, 3, _lib.F32) == _lib.EINVAL
+    assert info(256, 256, 1, _lib.F32) == (2, 1)
+
+
+def test_sdpa_shape_policy():
+    """The launch shape bi_sdpa picks on a 256-CU GPU for representative
+    problems (a performance policy; every shape gives the same bits, which the
+    GPU tests prove by forcing each one)."""
+    L = _lib.lib()
+
+    def pick(B, qL, H=32, Hkv=8, D=128, V=128, dtype=_lib.BF16):
+        return L.bi_sdpa_pick_shape(B, H, Hkv, qL, D, V, dtype, 256)
+
+    assert pick(64, 1) == pick(32, 1) == _lib.SDPA_TILE  # configs[2] decode, B >= 32
+    assert pick(16, 1) == _lib.SDPA_SPLIT2
+    assert pick(8, 1) == _lib.SDPA_SPLIT4
+    assert pick(1, 1) == pick(4, 1) == _lib.SDPA_SPLIT8  # dims over 8 workgroups
+    assert pick(1, 16) == _lib.SDPA_SPLIT8      # configs[3] chunk of 16 query rows
+    assert pick(1, 64) == _lib.SDPA_SPLIT2      # 8 streams x 16 tiles: too few for rows
+    assert pick(4, 64) == pick(1, 256) == _lib.SDPA_ROWS  # prefill: rows fill 256 CUs
+    assert pick(1, 2048) == pick(2, 513) == _lib.SDPA_ROWS
+    assert pick(1, 2048, D=256, V=256) == _lib.SDPA_ROWS
+    assert pick(64, 1, dtype=_lib.F32) == 2     # fp32: four query heads per workgroup
+    assert pick(1, 2048, dtype=_lib.F32) == 1   # fp32 prefill: two
+    assert pick(1, 1, dtype=_lib.F32) == 0
+    assert pick(1, 1, D=96, V=64) == _lib.EUNSUPPORTED
 
 
 def test_status_codes_map_to_reference_exceptions():
@@ -125,11 +186,16 @@ def test_status_codes_map_to_reference_exceptions():
 def test_tile_contract_is_pinned():
     """Guard against anyone changing the per-element arithmetic (the analogue
     of reference tests/test_invariance.py:468-470)."""
-    assert bi.TILE == dict(MFMA_16BIT="v_mfma_f32_16x16x32", MFMA_FP32="v_mfma_f32_16x16x4_f32",
+    assert bi.TILE == dict(BM=16, BN=16, BK=32, SG_M=1, SG_N=1,
+                           MFMA_16BIT="v_mfma_f32_16x16x32", MFMA_FP32="v_mfma_f32_16x16x4_f32",
                            K_CHUNK_16BIT=32, K_CHUNK_FP32=16, FP32_CHAINS=2,
                            EPILOGUE="fma(alpha, acc, beta * bias) then one RNE rounding")
+    # The reference's keys are all there, with the unit of fixed arithmetic.
+    assert {"BM", "BN", "BK", "SG_M", "SG_N"} <= set(bi.TILE)
+    assert bi.TILE["BK"] == bi.TILE["K_CHUNK_16BIT"]
     assert _attention.PARTIALS == 32 and _attention.GROUP_LANES == 8
-    assert bi.HEAD_DIMS == (64, 128, 256)
+    assert bi.HEAD_DIMS == ((32, 32), (64, 64), (96, 96), (128, 128), (160, 160), (192, 192),
+                            (224, 224), (256, 256), (192, 128))
 
 
 # ------------------------------------------------------------ Python validation
@@ -169,8 +235,10 @@ def test_sdpa_validation_matches_reference():
         bi.scaled_dot_product_attention(_t(1, 6, 2, 64), _t(1, 4, 16, 64), _t(1, 4, 16, 64))
     with pytest.raises(ValueError, match="multiples of 32"):
         bi.scaled_dot_product_attention(_t(1, 4, 1, 48), _t(1, 4, 8, 48), _t(1, 4, 8, 48))
-    with pytest.raises(NotImplementedError, match="not built"):
-        bi.scaled_dot_product_attention(_t(1, 4, 1, 96), _t(1, 4, 8, 96), _t(1, 4, 8, 96))
+    with pytest.raises(NotImplementedError, match="not built"):  # D != V pairs not compiled
+        bi.scaled_dot_product_attention(_t(1, 4, 1, 96), _t(1, 4, 8, 96), _t(1, 4, 8, 64))
+    with pytest.raises(NotImplementedError, match="not built"):  # above 256
+        bi.scaled_dot_product_attention(_t(1, 4, 1, 288), _t(1, 4, 8, 288), _t(1, 4, 8, 288))
     with pytest.raises(ValueError, match="sinks"):  # reference tests:355-364
         bi.scaled_dot_product_attention(q, k, v, sinks=torch.zeros(4))
     with pytest.raises(ValueError, match="causal"):
