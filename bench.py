@@ -133,7 +133,7 @@ def cpu_baseline(ops):
 
 
 def model_determinism(torch, bi, dev):
-    """configs[5]: random-init 32-layer Llama-shaped decoder, 512-token seeded
+    """configs[4]: random-init 32-layer Llama-shaped decoder, 512-token seeded
     prompt; bits of sequence 0's last-position logits at batch 8 vs batch 1,
     under batch_invariant_mode and stock; and the prefill time of both paths
     at batch 8 (HIP events, median of 3)."""
@@ -141,7 +141,7 @@ def model_determinism(torch, bi, dev):
 
     m = decoder.build(decoder.LLAMA_7B_SHAPE, device=dev, seed=0)
     ids = decoder.prompts(m.c, 8, 512, seed=0, device=dev)
-    out = {"config": "configs[5]: %d layers, hidden %d, %d/%d heads, FFN %d, vocab %d, bf16, "
+    out = {"config": "configs[4]: %d layers, hidden %d, %d/%d heads, FFN %d, vocab %d, bf16, "
                      "512-token prompt; sequence 0 at batch 8 vs batch 1"
                      % (m.c.layers, m.c.hidden, m.c.heads, m.c.kv_heads, m.c.inter, m.c.vocab)}
     for label, inv in (("invariant", True), ("stock", False)):
@@ -169,7 +169,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-model", action="store_true",
-                    help="skip the 32-layer decoder determinism check (configs[5])")
+                    help="skip the 32-layer decoder determinism check (configs[4])")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy three times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -183,7 +183,9 @@ def main():
 
     import mlx_batch_invariant as bi
     from mlx_batch_invariant import _gemm
-    from oracle.bits import bits
+
+    def bits(t):  # raw bit pattern of a 16-bit float tensor
+        return t.detach().contiguous().view(torch.int16).cpu()
 
     dev = torch.device("cuda:0")
     if args.calibrate_copy:

@@ -66,6 +66,28 @@ def test_batch_invariance_sweep(cuda, op):
                         op, dname, K, N, B, idx, d)
 
 
+def test_config2_widest_shape_sweep(cuda):
+    """BASELINE configs[1] at its widest (K, N) = (4096, 32000), (M,K)x(K,N),
+    N(0,1/K) weights, M in {1, 2, 4, ..., 256}, all three dtypes: the row at
+    positions 0, M//2 and M-1 has its M=1 bits. M = 256 takes the bench's
+    dominant 256 x 128 footprint; smaller M cross every other footprint."""
+    K, N = 4096, 32000
+    for dname, dtype in DTYPES:
+        W = rn((K, N), dtype, 1, std=K ** -0.5, device=cuda)
+        ref = rn((1, K), dtype, 3, device=cuda)
+        pool = rn((256, K), dtype, 2, device=cuda)
+        base = bi.matmul(ref, W)
+        assert bool((base != 0).any())
+        base = bits(base[0])
+        for M in (2, 4, 8, 16, 32, 64, 128, 256):
+            for idx in sorted({0, M // 2, M - 1}):
+                y = bi.matmul(batch_with(ref, pool, M, idx), W)
+                d = int((bits(y[idx]) != base).sum())
+                assert d == 0, "%s M=%d idx=%d: %d differ" % (dname, M, idx, d)
+        del W, pool
+        torch.cuda.empty_cache()
+
+
 def test_every_row_slot(cuda):
     """A row gives the same bits in every slot of every tile: a batch made of
     copies of one row must return copies of that row's B=1 result."""
@@ -139,7 +161,8 @@ def test_leading_dims_collapse_invariantly(cuda):
 
 
 ACC_CASES = [(17, 1024, 512), (128, 2048, 256), (1, 4096, 512), (8, 11008, 4096),
-             (128, 11008, 4096), (256, 4096, 4096)]
+             (128, 11008, 4096), (256, 4096, 4096),
+             (256, 4096, 32000), (1, 4096, 32000)]   # configs[1]'s widest shape
 
 
 def test_fp32_accuracy(cuda):

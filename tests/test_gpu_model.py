@@ -1,7 +1,7 @@
 """End-to-end determinism on the synthetic decoder (mlx_batch_invariant.decoder):
 under batch_invariant_mode, sequence 0's logits have the same bits at batch
-1, 2, 4 and 8 (reference bench/bench.py:217-246). A reduced configuration
-keeps the test quick; bench.py runs the full 32-layer shape."""
+1, 2, 4 and 8 (reference bench/bench.py:217-246), on a reduced configuration
+and on the full 32-layer configs[4] shape."""
 
 import pytest
 import torch
@@ -19,6 +19,22 @@ def test_decoder_logits_invariant_across_batch(cuda):
     m = decoder.build(SMALL, device=cuda, seed=0)
     got = decoder.determinism(m, length=96, batches=(2, 4, 8), seed=1, invariant=True)
     assert got == {2: 0, 4: 0, 8: 0}, got
+
+
+def test_full_config_decoder_logits(cuda):
+    """BASELINE configs[4] at full size (32 layers, hidden 4096, 32/8 heads, FFN
+    11008, vocabulary 32000, bf16, 512-token seeded prompt; reference
+    bench/bench.py:217-246): sequence 0's logits at batch 8 have the bits of
+    batch 1 under the mode (0 of 32000 differ), and stock torch differs."""
+    m = decoder.build(decoder.LLAMA_7B_SHAPE, device=cuda, seed=0)
+    try:
+        got = decoder.determinism(m, length=512, batches=(8,), seed=0, invariant=True)
+        stock = decoder.determinism(m, length=512, batches=(8,), seed=0, invariant=False)
+    finally:
+        del m
+        torch.cuda.empty_cache()
+    assert got == {8: 0}, got
+    assert stock[8] > 0, "stock torch came out invariant: the check proves nothing"
 
 
 def test_decoder_routes_through_the_invariant_kernels(cuda):

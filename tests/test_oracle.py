@@ -107,6 +107,19 @@ def test_gemm_f64_against_brute_force():
                        atol=0)
 
 
+def test_abs_products_against_brute_force():
+    """The cancellation floor's scale is sum_k |a[m, k] * b[k, n]| -- not
+    |sum_k a b| (which cancellation drives to 0) -- in both layouts."""
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((3, 6))
+    b = rng.standard_normal((6, 5))
+    want = [[sum(abs(a[m, k] * b[k, n]) for k in range(6)) for n in range(5)] for m in range(3)]
+    assert np.allclose(ogemm.abs_products(a, b), want, rtol=1e-14, atol=0)
+    assert np.allclose(ogemm.abs_products(a, b.T, trans_b=True), want, rtol=1e-14, atol=0)
+    # A cancelling row: the floor stays at the size of the terms.
+    assert ogemm.abs_products(np.array([[1.0, -1.0]]), np.array([[3.0], [3.0]]))[0, 0] == 6.0
+
+
 def test_gemm_fixed32_is_sequential_k_ascending():
     """In fp32, 1 - 1e8 rounds to -1e8. Terms (1e8, -1e8, 1) summed in
     ascending k give (1e8 - 1e8) + 1 = 1; summed from the other end they give
