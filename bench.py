@@ -11,14 +11,21 @@ resident in HBM. Alongside, on the same run:
     duration over the timed steps from HIP events that the launch itself
     records (the kernel's own start and end timestamps);
   * stock torch.matmul (hipBLASLt) on the same inputs, interleaved;
-  * decode SDPA (configs[2]: B = 64, 32/8 heads, D = 128, N = 8192) GB/s;
+  * the same sweep in f16 and fp32 (fp32 against the 157.3 TFLOP/s fp32
+    MFMA peak);
+  * decode SDPA (configs[2]: B = 64, 32/8 heads, D = 128, N = 8192) GB/s, and
+    a decode sweep over B in {1, 8, 64} x N in {2048, 8192};
   * causal prefill SDPA (B = 1, 32/8 heads, D = 128, 2048 x 2048) TFLOP/s,
     against stock torch SDPA;
   * 4-bit affine quantized linear (4096 x 4096, group 64) at M = 1 and 256,
     against stock dequantize + F.linear;
-  * a bit-invariance check of one row across batch sizes 1..256;
-  * the CPU baseline: the oracle's fixed-order fp32 restatement of the
-    reference GEMM (C, OpenMP) on a bounded sample of the same workload.
+  * a bit-invariance check of row 0 of every shape across batch sizes 1..256;
+  * the CPU baseline on the host cores this process may use: the oracle's
+    fixed-order fp32 restatements of the reference GEMM and attention (C,
+    OpenMP) on bounded samples of the same workloads, beside stock torch.
+Every GPU entry carries its roofline fraction: achieved / min(MFMA peak,
+arithmetic intensity x HBM peak) for the GEMMs and prefill attention, and
+achieved / HBM peak for decode attention and the quantized linear.
 Prints one JSON line.
 """
 
@@ -40,10 +47,13 @@ M = 256
 SHAPES = [(512, 512), (4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)]  # (K, N)
 DOMINANT = (4096, 32000)
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}  # dense MFMA peaks
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 SDPA = dict(B=64, H=32, Hkv=8, N=8192, D=128)
 CPU_ROWS = 256              # rows of M per shape in the CPU sample (all of them)
 CPU_SECONDS = 10.0          # repeat whole passes until at least this long
+CPU_SDPA_B = 4              # batch entries of configs[2] in the CPU attention sample
+CPU_SDPA_SECONDS = 5.0
 
 
 def gemm_flops(m, k, n):
@@ -58,14 +68,43 @@ def sdpa_bytes(B, H, Hkv, N, D, esize=2):
     return float(2 * B * Hkv * N * D + 2 * B * H * 1 * D) * esize
 
 
-def make_inputs(torch, dev):
-    g = torch.Generator().manual_seed(0)
+def make_inputs(torch, dev, dtype=None, seed=0):
+    dtype = dtype or torch.bfloat16
+    g = torch.Generator().manual_seed(seed)
     ops = []
     for K, N in SHAPES:
-        a = torch.randn(M, K, generator=g).to(torch.bfloat16)
-        w = (torch.randn(K, N, generator=g) / math.sqrt(K)).to(torch.bfloat16)
+        a = torch.randn(M, K, generator=g).to(dtype)
+        w = (torch.randn(K, N, generator=g) / math.sqrt(K)).to(dtype)
         ops.append((a, w, a.to(dev), w.to(dev)))
     return ops
+
+
+def gemm_roof(m, k, n, us, dname="bf16"):
+    """Roofline figures of one GEMM launch of `us` microseconds."""
+    es = 4 if dname == "f32" else 2
+    fl, by = gemm_flops(m, k, n), gemm_bytes(m, k, n, es)
+    tf = fl / us / 1e6
+    roof = min(PEAK_TFLOPS[dname], fl / by * PEAK_HBM_GBS / 1e3)
+    return {"tflops": round(tf, 1), "gbps": round(by / us / 1e3, 1),
+            "frac_of_min_roof": round(tf / roof, 4),
+            "mfma_frac": round(tf / PEAK_TFLOPS[dname], 4),
+            "hbm_frac": round(by / us / 1e3 / PEAK_HBM_GBS, 4),
+            "bound": "hbm" if roof < PEAK_TFLOPS[dname] else "mfma"}
+
+
+def host_cores():
+    """(cores this process may use, cores visible): the affinity mask, capped by
+    the cgroup CPU quota where one is set (a GPU box's share of a larger host)."""
+    vis = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(per)))
+    except (OSError, ValueError):
+        pass
+    return (min(vis, quota) if quota else vis), vis
 
 
 def load_traffic():
@@ -81,9 +120,11 @@ def load_traffic():
 
 
 def cpu_baseline(ops):
-    """Oracle fixed-order fp32 GEMM (C, OpenMP, all usable cores up to 16) on
-    the first CPU_ROWS rows of every shape of the step."""
-    cores = min(16, len(os.sched_getaffinity(0)))
+    """Oracle fixed-order fp32 GEMM (C, OpenMP, every core this process may
+    use) on the first CPU_ROWS rows of every shape of the step; the oracle's
+    fixed-order attention on CPU_SDPA_B batch entries of configs[2]; stock
+    torch on the same samples."""
+    cores, visible = host_cores()
     os.environ["OMP_NUM_THREADS"] = str(cores)
     import numpy as np
 
@@ -121,15 +162,51 @@ def cpu_baseline(ops):
             tflops += gemm_flops(CPU_ROWS, a32.shape[1], b32.shape[1])
         tpasses += 1
     tdt = time.perf_counter() - t1
+    sdpa = cpu_sdpa_baseline(torch, np)
     mlx = importlib.util.find_spec("mlx") is not None
     return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": cores,
+            "cores_visible": visible,
             "kind": "port",
             "sample": "%d pass(es) over the first %d of the %d rows of each of the 5 (K,N) "
                       "shapes; fixed-order fp32 fmaf restatement of the reference K loop "
-                      "(oracle/csrc/oracle.c), %.1f s" % (passes, CPU_ROWS, M, dt),
+                      "(oracle/csrc/oracle.c), %.1f s on %d threads" % (passes, CPU_ROWS, M, dt,
+                                                                         cores),
             "torch_cpu_tflops": round(tflops / tdt / 1e12, 4),
+            "sdpa": sdpa,
             "mlx_cpu": ("mlx is importable but its CPU timing is not built in this bench"
                         if mlx else "unavailable: mlx is not installed on this host")}
+
+
+def cpu_sdpa_baseline(torch, np):
+    """configs[2] decode attention on the host: the oracle's fixed-order fp32
+    restatement of the reference kernel (32 key-stride partials, C, OpenMP over
+    batch x head x row) and stock torch CPU SDPA, on CPU_SDPA_B of the 64 batch
+    entries, reported as the algorithmic bytes of the sample per second."""
+    from oracle import sdpa as osdpa
+
+    B, H, Hkv, N, D = CPU_SDPA_B, SDPA["H"], SDPA["Hkv"], SDPA["N"], SDPA["D"]
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(B, H, 1, D, generator=g).to(torch.bfloat16).float().numpy()
+    k = torch.randn(B, Hkv, N, D, generator=g).to(torch.bfloat16).float().numpy()
+    v = torch.randn(B, Hkv, N, D, generator=g).to(torch.bfloat16).float().numpy()
+    by = sdpa_bytes(B, H, Hkv, N, D)
+    passes, t0 = 0, time.perf_counter()
+    while passes == 0 or time.perf_counter() - t0 < CPU_SDPA_SECONDS:
+        osdpa.sdpa_fixed32(q, k, v, scale=1.0 / math.sqrt(D))
+        passes += 1
+    dt = time.perf_counter() - t0
+    tq, tk, tv = (torch.from_numpy(x) for x in (q, k, v))
+    tpasses, t1 = 0, time.perf_counter()
+    while tpasses == 0 or time.perf_counter() - t1 < 2.0:
+        torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, enable_gqa=True)
+        tpasses += 1
+    tdt = time.perf_counter() - t1
+    return {"value": round(by * passes / dt / 1e9, 3), "unit": "GB/s",
+            "sample": "%d pass(es) over %d of the 64 batch entries of configs[2] (32/8 heads, "
+                      "D=128, N=8192, qL=1), bytes counted as bf16 like the GPU figure; "
+                      "fixed-order fp32 restatement of the reference attention "
+                      "(oracle/csrc/oracle.c), %.1f s" % (passes, B, dt),
+            "torch_cpu_gbps": round(by * tpasses / tdt / 1e9, 3)}
 
 
 def model_determinism(torch, bi, dev):
@@ -257,8 +334,33 @@ def main():
                           "bi_tflops": round(gemm_flops(M, K, N) / tb / 1e6, 1),
                           "stock_us": round(ts, 2),
                           "stock_tflops": round(gemm_flops(M, K, N) / ts / 1e6, 1),
+                          "roofline": gemm_roof(M, K, N, tb),
                           "geometry": _gemm.geometries()[
                               _gemm._lib.lib().bi_gemm_pick_geometry(M, N, K, 2, 0)]})
+
+    # The same sweep in f16 and fp32 (fp32 against its own MFMA peak): HIP
+    # events around whole steps, after a warmup.
+    other_dtypes = {}
+    for dname, dt in (("f16", torch.float16), ("f32", torch.float32)):
+        ops_d = make_inputs(torch, dev, dt)
+        for _ in range(3):
+            for _, _, a, w in ops_d:
+                bi.matmul(a, w)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        nrep = 10
+        e0.record()
+        for _ in range(nrep):
+            for _, _, a, w in ops_d:
+                bi.matmul(a, w)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / nrep
+        tf = step_flops / ms / 1e9
+        other_dtypes[dname] = {"ms_per_step": round(ms, 4), "tflops": round(tf, 1),
+                               "mfma_frac": round(tf / PEAK_TFLOPS[dname], 4),
+                               "peak_tflops": PEAK_TFLOPS[dname]}
+        del ops_d
+    torch.cuda.empty_cache()
 
     # Roofline of the dominant kernel: AI below the bf16 ridge, so HBM binds.
     Kd, Nd = DOMINANT
@@ -292,6 +394,25 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(sbytes / sd_bi / 1e3, 1),
                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(sbytes / sd_bi / 1e3 / PEAK_HBM_GBS, 4)}}
+    del q, k, v
+    # Decode sweep over configs[2]'s range: B in {1, 8, 64} x N in {2048, 8192}.
+    sweep = []
+    for Bd in (1, 8, 64):
+        for Nd in (2048, 8192):
+            qd = torch.randn(Bd, H, 1, D, generator=g).to(torch.bfloat16).to(dev)
+            kd = torch.randn(Bd, Hkv, Nd, D, generator=g).to(torch.bfloat16).to(dev)
+            vd = torch.randn(Bd, Hkv, Nd, D, generator=g).to(torch.bfloat16).to(dev)
+            t_bi = statistics.median(time_us(lambda: bi.scaled_dot_product_attention(
+                qd, kd, vd, scale=sc), reps=10) for _ in range(5))
+            t_st = statistics.median(time_us(lambda: torch.nn.functional.scaled_dot_product_attention(
+                qd, kd, vd, scale=sc, enable_gqa=True), reps=10) for _ in range(5))
+            by_d = sdpa_bytes(Bd, H, Hkv, Nd, D)
+            sweep.append({"B": Bd, "N": Nd, "bi_us": round(t_bi, 1),
+                          "gbps": round(by_d / t_bi / 1e3, 1),
+                          "hbm_frac": round(by_d / t_bi / 1e3 / PEAK_HBM_GBS, 4),
+                          "stock_us": round(t_st, 1)})
+            del qd, kd, vd
+    sdpa["sweep"] = sweep
 
     # Causal prefill attention (the query-row-blocked path of the same kernel):
     # B=1, 32/8 heads, D=128, 2048 query rows over 2048 keys.
@@ -304,9 +425,14 @@ def main():
     pf_st = statistics.median(time_us(lambda: torch.nn.functional.scaled_dot_product_attention(
         qp, kp, vp, scale=sc, is_causal=True, enable_gqa=True), reps=5) for _ in range(5))
     pf_flops = 4 * H * L * L * D / 2  # QK^T and PV over the causal half
+    pf_bytes = float(2 * H * L * D + 2 * 2 * Hkv * L * D) * 2  # q, out, k, v once each
+    pf_roof = min(PEAK_BF16_TFLOPS, pf_flops / pf_bytes * PEAK_HBM_GBS / 1e3)
     prefill = {"config": dict(B=1, H=H, Hkv=Hkv, qL=L, N=L, D=D, mask="causal", dtype="bf16"),
                "bi_us": round(pf_bi, 1), "bi_tflops": round(pf_flops / pf_bi / 1e6, 1),
-               "stock_us": round(pf_st, 1), "stock_tflops": round(pf_flops / pf_st / 1e6, 1)}
+               "stock_us": round(pf_st, 1), "stock_tflops": round(pf_flops / pf_st / 1e6, 1),
+               "roofline": {"bound": "mfma" if pf_roof >= PEAK_BF16_TFLOPS else "hbm",
+                            "frac_of_min_roof": round(pf_flops / pf_bi / 1e6 / pf_roof, 4),
+                            "mfma_frac": round(pf_flops / pf_bi / 1e6 / PEAK_BF16_TFLOPS, 4)}}
 
     # Affine 4-bit quantized linear (group 64), 4096 x 4096 weight: decode and
     # M=256 rows; stock is dequantize + F.linear.
@@ -319,14 +445,23 @@ def main():
                                  for _ in range(5))
         q_st = statistics.median(time_us(lambda: torch.nn.functional.linear(
             xq, bi.dequantize(qw, qs, qz, 64, 4))) for _ in range(5))
-        quant["M%d" % Mq] = {"bi_us": round(q_bi, 1), "stock_us": round(q_st, 1)}
+        # Algorithmic bytes: activations, packed weight, scales and biases, output.
+        q_bytes = float(Mq * 4096 * 2 + 4096 * 4096 // 2 + 2 * 4096 * (4096 // 64) * 2
+                        + Mq * 4096 * 2)
+        q_flops = 2.0 * Mq * 4096 * 4096
+        q_roof = min(PEAK_BF16_TFLOPS, q_flops / q_bytes * PEAK_HBM_GBS / 1e3)
+        quant["M%d" % Mq] = {"bi_us": round(q_bi, 1), "stock_us": round(q_st, 1),
+                             "gbps": round(q_bytes / q_bi / 1e3, 1),
+                             "tflops": round(q_flops / q_bi / 1e6, 2),
+                             "frac_of_min_roof": round(q_flops / q_bi / 1e6 / q_roof, 4)}
 
-    # Invariance spot check: row 0 of the (4096, 4096) shape across batch sizes.
-    a, w = ops[1][2], ops[1][3]
-    ref = bits(bi.matmul(a[:1].contiguous(), w)[0])
+    # Invariance spot check: row 0 of every shape of the sweep across batch
+    # sizes 1..256 (each batch size picks its own workgroup footprint).
     differing = 0
-    for b in (2, 3, 8, 16, 33, 64, 128, 256):
-        differing += int((bits(bi.matmul(a[:b].contiguous(), w)[0]) != ref).sum())
+    for _, _, a, w in ops:
+        ref = bits(bi.matmul(a[:1].contiguous(), w)[0])
+        for b in (2, 3, 8, 16, 17, 33, 64, 65, 128, 255, 256):
+            differing += int((bits(bi.matmul(a[:b].contiguous(), w)[0]) != ref).sum())
 
     model = None if args.no_model else model_determinism(torch, bi, dev)
     cpu = None if args.no_cpu else cpu_baseline(ops)
@@ -341,6 +476,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "per_shape": per_shape,
+        "sweep_other_dtypes": other_dtypes,
         "sdpa_decode": sdpa,
         "sdpa_prefill": prefill,
         "quantized_linear": quant,
