@@ -28,11 +28,12 @@
 //     f = m' == m ? 1 : exp2(m - m'),
 //     p_i = exp2(s_i - m') (0 for unused keys), l = fma(l, f, sum_i p_i) with
 //     the block sum taken in a fixed tree; o = o * f + 0.0 (skipped when
-//     f == 1, which changes no bits), then o += p . v as v_mfma_f32_16x16x16 with p
-//     split into hi and lo = T(p - hi), hi = p truncated to bf16 (bf16) or
-//     T(p) (f16): for each 16-dim block, keys
-//     0-15 hi, keys 0-15 lo, keys 16-31 hi, keys 16-31 lo. m starts at the
-//     lowest finite float and l at 0 (reference :76-79).
+//     f == 1, which changes no bits), then o += p . v as two
+//     v_mfma_f32_16x16x32_{bf16,f16} over the block's 32 keys per 16-dim block,
+//     first with p's hi plane, then with its lo plane = T(p - hi), hi = p
+//     truncated to bf16 (bf16) or T(p) (f16); in both, lane group g supplies
+//     keys 4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3. m starts at the lowest
+//     finite float and l at 0 (reference :76-79).
 //   * Merge: a sink (reference :80-86, an extra denominator term exp(sink))
 //     enters here as one more partial with m = sink * log2 e, l = 1, o = 0,
 //     ahead of the chains: M = max of the sink's and the chains' m;
@@ -108,16 +109,8 @@ __device__ inline f32x4_t mma32(_Float16, uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
-// 16x16x16: lane (r, g) supplies A[r][4g + t] and B[4g + t][r], t = 0..3;
-// it receives C[4g + e][r].
-__device__ inline f32x4_t mma16(__bf16, uint2 a, uint2 b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, a),
-                                                   __builtin_bit_cast(i16x4_t, b), c, 0, 0, 0);
-}
-__device__ inline f32x4_t mma16(_Float16, uint2 a, uint2 b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
-                                               __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
-}
+// Two 4-element halves as one 8-element MFMA operand (elements 0-3 from lo).
+__device__ inline uint4 join(uint2 lo, uint2 hi) { return make_uint4(lo.x, lo.y, hi.x, hi.y); }
 
 // ds_read_b64_tr_b16 (in each 16-lane group, lane i receives element i of
 // the four 4 x 16-bit rows its group addresses, one per row) as an asm
@@ -647,16 +640,17 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
         for (int db = 0; db < NB; db++) va[db][kt] &= vm;
       }
     }
+    // o += P . V over the block's 32 keys: A = V^T (16 dims x 32 keys), lane
+    // (r16, g) holding keys 4g + t and 16 + 4g + t of dim 16db + r16; B = P^T
+    // with the same keys of column r16 -- the 16x16x32 operand layout with K
+    // slots 0-3 and 4-7 of lane group g taken by those two key quads.
 #pragma unroll
     for (int db = 0; db < NB; db++) {
+      const uint4 vt = join(__builtin_bit_cast(uint2, va[db][0]), __builtin_bit_cast(uint2, va[db][1]));
 #pragma unroll
-      for (int kt = 0; kt < 2; kt++) {
-        const uint2 v2 = __builtin_bit_cast(uint2, va[db][kt]);
-#pragma unroll
-        for (int ct = 0; ct < CT; ct++) {
-          o[ct][db] = mma16(T(0), v2, ph[ct][kt], o[ct][db]);
-          o[ct][db] = mma16(T(0), v2, pl[ct][kt], o[ct][db]);
-        }
+      for (int ct = 0; ct < CT; ct++) {
+        o[ct][db] = mma32(T(0), vt, join(ph[ct][0], ph[ct][1]), o[ct][db]);
+        o[ct][db] = mma32(T(0), vt, join(pl[ct][0], pl[ct][1]), o[ct][db]);
       }
     }
   };
