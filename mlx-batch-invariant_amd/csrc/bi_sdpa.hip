@@ -1,5 +1,5 @@
 // Batch-invariant single-pass scaled dot product attention for gfx950: the
-// fp32 kernel (bf16 and f16 run on matrix cores, bi_sdpa_mfma.hip), and the
+// fp32 kernel (bf16 and f16 run on matrix cores, bi_sdpa_mfma_kernel.h), and the
 // C entry point bi_sdpa that validates arguments and launches either.
 //
 // Restates the reference bi_sdpa (mlx_batch_invariant/_attention.py:32-149):

@@ -1,6 +1,6 @@
 // Batch-invariant single-pass attention on MFMA (gfx950), bf16 and f16: the
 // kernel template, included by one instantiation unit per built head-dim pair
-// (bi_sdpa_mfma_d*.hip); bi_sdpa_mfma.hip chooses the launch shape.
+// (bi_sdpa_mfma_d*.hip); bi_sdpa.hip chooses the launch shape.
 //
 // Restates the reference bi_sdpa (mlx_batch_invariant/_attention.py:32-149)
 // with matrix cores: one workgroup owns the whole key reduction for each of
