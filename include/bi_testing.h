@@ -63,14 +63,17 @@ int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
  * Shapes of BI_F16 / BI_BF16: 0 "rows" (prefill: 2 column tiles per
  * workgroup, 1 for head dims above 128), 1 one tile, 2 / 3 / 4 one tile with
  * the output dims split over 2 / 4 / 8 workgroups (fewer where the value
- * head dim does not allow it). Shapes of BI_F32: s = 0..3, 2^s query heads
- * per workgroup.
+ * head dim does not allow it), 5 "shared" (prefill without an array mask,
+ * D and V in {32, 64, 128}: one column tile per wave, 4 or 8 waves reading
+ * each key and value block once from LDS). Shapes of BI_F32: s = 0..3, 2^s
+ * query heads per workgroup.
  */
 
-/* The shape bi_sdpa picks for this problem on a GPU of `cus` compute units
- * (0: the current device's). Returns the shape (>= 0) or a negative status. */
+/* The shape bi_sdpa picks for this problem (mask_mode as for bi_sdpa) on a
+ * GPU of `cus` compute units (0: the current device's). Returns the shape
+ * (>= 0) or a negative status. */
 int bi_sdpa_pick_shape(int64_t B, int64_t H, int64_t Hkv, int64_t qL, int64_t D, int64_t V,
-                       int dtype, int cus);
+                       int dtype, int mask_mode, int cus);
 
 /* Columns (BI_F32: query heads) and output-dim splits per workgroup of a
  * shape; BI_EINVAL if that shape is not built for the head dims. */

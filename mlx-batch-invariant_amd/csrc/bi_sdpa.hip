@@ -376,11 +376,20 @@ SdpaKernelFn mfma_kernel(int64_t D, int64_t V, int dtype, bool mask, int shape) 
   return nullptr;
 }
 
-// "Rows" when a kv head has more than 16 columns (prefill) and that grid fills
-// the compute units; otherwise one column tile, with the output dims split
-// over 2, 4 or 8 workgroups when the grid of column tiles would leave compute
-// units idle: decode, and short chunks of prefill such as 16 query rows.
-int mfma_pick_shape(int64_t D, int64_t V, int64_t ncol, int64_t streams, int cus) {
+// Prefill (a kv head has more than 16 columns): "shared" for D = V = 128
+// without an array mask when its grid of 128-column workgroups gives every
+// compute unit two (L = 2048 causal: 113 -> 92 us; at D = 64 and 32, or on
+// smaller grids, it measured slower than rows), else "rows" when that grid
+// fills the compute units. Otherwise one
+// column tile, with the output dims split over 2, 4 or 8 workgroups when the
+// grid of column tiles would leave compute units idle: decode, and short
+// chunks of prefill such as 16 query rows.
+int mfma_pick_shape(int64_t D, int64_t V, int64_t ncol, int64_t streams, bool array_mask,
+                    int cus) {
+  if (ncol > 16 && D == 128 && V == 128 && !array_mask) {
+    const int sc = sdpa_shape_columns(D, V, SDPA_SHARED);
+    if (streams * ((ncol + sc - 1) / sc) >= 2 * (int64_t)cus) return SDPA_SHARED;
+  }
   const int rc = sdpa_shape_columns(D, V, SDPA_ROWS);
   if (ncol > 16 && streams * ((ncol + rc - 1) / rc) >= cus) return SDPA_ROWS;
   const int64_t tiles = streams * ((ncol + 15) / 16);  // workgroups at one column tile
@@ -399,9 +408,9 @@ bool dims_built(int64_t D, int64_t V) {
 }
 
 int pick_shape(int64_t B, int64_t H, int64_t Hkv, int64_t qL, int64_t D, int64_t V, int dtype,
-               int cus) {
+               int mask_mode, int cus) {
   if (dtype == BI_F32) return f32_pick_shape(H / Hkv, D, V, B * H * qL, qL, cus);
-  return mfma_pick_shape(D, V, (H / Hkv) * qL, B * Hkv, cus);
+  return mfma_pick_shape(D, V, (H / Hkv) * qL, B * Hkv, mask_mode == BI_MASK_ARRAY, cus);
 }
 
 // Columns (query heads for fp32, (head, row) columns otherwise) and output-dim
@@ -496,7 +505,7 @@ int sdpa_run(const void* q, const void* k, const void* v, const void* mask,
         ((H - 1) * p.ms[1] + (qL - 1) * p.ms[2] + N + kMaskSlack) * esz > INT32_MAX)
       return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: the mask of one batch entry is too large");
   }
-  if (shape < 0) shape = pick_shape(B, H, Hkv, qL, D, V, dtype, device_cus());
+  if (shape < 0) shape = pick_shape(B, H, Hkv, qL, D, V, dtype, mask_mode, device_cus());
   int columns = 0, splits = 0;
   if (!shape_geometry(D, V, dtype, shape, &columns, &splits))
     return bi::fail(BI_EINVAL, "bi_sdpa: launch shape %d is not built for dtype %d D=%lld V=%lld",
@@ -517,7 +526,10 @@ int sdpa_run(const void* q, const void* k, const void* v, const void* mask,
     blocks = B * Hkv * ((ncol + columns - 1) / columns) * splits;
   }
   if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_sdpa: grid too large");
-  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), 0,
+  if (!fn)
+    return bi::fail(BI_EINVAL, "bi_sdpa: launch shape %d is not built for this mask", shape);
+  const int threads = dtype == BI_F32 ? kThreads : sdpa_shape_threads(D, V, shape);
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(threads), 0,
                      static_cast<hipStream_t>(hip_stream), p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return bi::launch_error(e, "bi_sdpa launch");
@@ -547,14 +559,16 @@ extern "C" int bi_sdpa_with_shape(const void* q, const void* k, const void* v, c
 }
 
 extern "C" int bi_sdpa_pick_shape(int64_t B, int64_t H, int64_t Hkv, int64_t qL, int64_t D,
-                                  int64_t V, int dtype, int cus) {
+                                  int64_t V, int dtype, int mask_mode, int cus) {
   if (!bi::elem_size(dtype)) return bi::fail(BI_EINVAL, "bi_sdpa_pick_shape: unknown dtype %d", dtype);
   if (B <= 0 || H <= 0 || Hkv <= 0 || qL <= 0 || H % Hkv || cus < 0)
     return bi::fail(BI_EINVAL, "bi_sdpa_pick_shape: bad sizes");
+  if (mask_mode != BI_MASK_NONE && mask_mode != BI_MASK_CAUSAL && mask_mode != BI_MASK_ARRAY)
+    return bi::fail(BI_EINVAL, "bi_sdpa_pick_shape: unknown mask mode %d", mask_mode);
   if (!dims_built(D, V))
     return bi::fail(BI_EUNSUPPORTED, "bi_sdpa_pick_shape: head dims D=%lld V=%lld are not built",
                     (long long)D, (long long)V);
-  return pick_shape(B, H, Hkv, qL, D, V, dtype, cus > 0 ? cus : device_cus());
+  return pick_shape(B, H, Hkv, qL, D, V, dtype, mask_mode, cus > 0 ? cus : device_cus());
 }
 
 extern "C" int bi_sdpa_shape_info(int64_t D, int64_t V, int dtype, int shape, int* columns,

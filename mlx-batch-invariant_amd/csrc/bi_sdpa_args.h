@@ -32,13 +32,17 @@ typedef void (*SdpaKernelFn)(SdpaArgs);
 // Launch shapes of the MFMA kernel (bf16 / f16). None of them enters a
 // column's arithmetic; they decide which workgroup, wave and lane evaluate a
 // column and how operands travel.
-//   SDPA_ROWS    several 16-column tiles per workgroup (prefill)
+//   SDPA_ROWS    several 16-column tiles per workgroup, one chain per wave
 //   SDPA_TILE    one column tile, output dims whole (or split in two for V > 128)
 //   SDPA_SPLITn  one column tile, output dims split over n workgroups (decode),
 //                capped by the largest power of two that leaves each workgroup
 //                a multiple of 16 dims
+//   SDPA_SHARED  one 16-column tile per wave, every wave walking every key
+//                block with all 4 chains' state of its columns: a key and value
+//                block is loaded once into LDS for 4-8 column tiles (prefill;
+//                D and V in {32, 64, 128})
 enum SdpaShape { SDPA_ROWS = 0, SDPA_TILE = 1, SDPA_SPLIT2 = 2, SDPA_SPLIT4 = 3, SDPA_SPLIT8 = 4,
-                 SDPA_NUM_SHAPES = 5 };
+                 SDPA_SHARED = 5, SDPA_NUM_SHAPES = 6 };
 
 // Heads wider than 128 carry more registers per column: one column tile per
 // rows workgroup, no key prefetch, value dims always split at least in two.
@@ -48,13 +52,27 @@ constexpr int sdpa_splits_max(int64_t V) {
   return (V / 16) % 8 == 0 ? 8 : (V / 16) % 4 == 0 ? 4 : (V / 16) % 2 == 0 ? 2 : 1;
 }
 constexpr int sdpa_splits_min(int64_t V) { return V > 128 ? 2 : 1; }
+// SDPA_SHARED: built for D and V in {32, 64, 128}; its waves split the
+// (D + V) / 16 loads of a key block evenly, at most 8 waves.
+constexpr bool sdpa_shared_dims(int64_t D, int64_t V) {
+  return (D == 32 || D == 64 || D == 128) && (V == 32 || V == 64 || V == 128);
+}
+constexpr int sdpa_shared_waves(int64_t D, int64_t V) {
+  return (D + V) / 16 >= 8 ? 8 : (int)((D + V) / 16);
+}
 constexpr int sdpa_shape_splits(int64_t V, int shape) {
-  const int want = shape <= SDPA_TILE ? 1 : 1 << (shape - 1);
+  const int want = shape <= SDPA_TILE || shape == SDPA_SHARED ? 1 : 1 << (shape - 1);
   const int capped = want < sdpa_splits_max(V) ? want : sdpa_splits_max(V);
   return capped > sdpa_splits_min(V) ? capped : sdpa_splits_min(V);
 }
 constexpr int sdpa_shape_columns(int64_t D, int64_t V, int shape) {
-  return shape == SDPA_ROWS ? 16 * sdpa_rows_tiles(D, V) : 16;
+  return shape == SDPA_ROWS     ? 16 * sdpa_rows_tiles(D, V)
+         : shape == SDPA_SHARED ? 16 * sdpa_shared_waves(D, V)
+                                : 16;
+}
+// Threads per workgroup: 4 waves (one per chain), or one per column tile.
+constexpr int sdpa_shape_threads(int64_t D, int64_t V, int shape) {
+  return shape == SDPA_SHARED ? 64 * sdpa_shared_waves(D, V) : 256;
 }
 
 // The MFMA kernel of one head-dim pair for (dtype, array mask or not, shape);

@@ -131,6 +131,18 @@ __device__ __forceinline__ u32x4_t ds_read_b128(uint32_t lds_addr) {
   asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_addr) : "memory");
   return v;
 }
+// The same two reads at a lane address plus a constant (the instruction's
+// 16-bit offset field), so that unrolled reads share one address register.
+__device__ __forceinline__ u32x2_t ds_read_tr_at(uint32_t lds_addr, int off) {
+  u32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(lds_addr), "i"(off) : "memory");
+  return v;
+}
+__device__ __forceinline__ u32x4_t ds_read_b128_at(uint32_t lds_addr, int off) {
+  u32x4_t v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(lds_addr), "i"(off) : "memory");
+  return v;
+}
 
 template <typename T> __device__ inline unsigned short tbits(T x) {
   return __builtin_bit_cast(unsigned short, x);
@@ -738,6 +750,377 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   }
 }
 
+// f(integral_constant<I>) for I = I0 .. N - 1 while it returns true.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F& f) {
+  if constexpr (I < N) {
+    if (f(std::integral_constant<int, I>{})) static_for<I + 1, N>(f);
+  }
+}
+
+// Launch shape SDPA_SHARED (prefill without an array mask): NW waves, each
+// owning one tile of 16 columns, and every wave walks every key block of the
+// workgroup in ascending order, block b updating the state of chain b mod 4
+// that the wave keeps for its columns. A column's 4 chains, their blocks and
+// their arithmetic are those of the other shapes (the steps below are the
+// same operations in the same order as sdpa_mfma_kernel's), only evaluated
+// by one wave: a key and value block is loaded once, into LDS slots that all
+// waves read, for 16 * NW columns instead of 16 or 32.
+//
+// The slots form two groups of GP. The waves synchronise once per group:
+// at group g's barrier every wave's loads of group g have landed and every
+// wave has finished group g - 1, whose slots then take group g + 1's loads.
+// Between barriers the waves drift apart, so one wave's softmax overlaps
+// another's products on the same SIMD.
+template <typename T, int D, int V, int NW, int GP>
+struct Shared {
+  static constexpr int NQ = D / 32;        // score MFMAs per 16 keys
+  static constexpr int NB = V / 16;        // 16-dim blocks of o
+  static constexpr int CH = D / 8;         // 16-byte chunks per key row
+  static constexpr int VCH = V / 8;        // 16-byte chunks per value row
+  static constexpr int KSLOT = kBlk * CH;  // uint4 of keys per slot
+  static constexpr int SLOT = KSLOT + kBlk * VCH;  // uint4 per slot (keys, then values)
+  static constexpr int NL = SLOT / 64;     // LDS-DMA loads per block
+  static constexpr int LPW = NL / NW;      // of them issued by each wave
+  static constexpr int S = 2 * GP;         // slots
+  static constexpr int HALF = GP * SLOT * 16;  // bytes of one group's slots
+  // Whether the two groups need their own lane address registers (LDS read
+  // offsets are 16-bit immediates).
+  static constexpr bool TWO_BASES = 2 * HALF > 65536;
+  static_assert(NL % NW == 0 && (CH & (CH - 1)) == 0 && (VCH & (VCH - 1)) == 0 && D <= 128 &&
+                    V <= 128 && VCH >= 4 && (4 % GP == 0 || GP % 4 == 0),
+                "shape");
+  static_assert(GP * LPW <= 63, "loads in flight exceed the vmcnt range");
+  static_assert(S * SLOT * 16 <= 160 * 1024 && HALF <= 65536, "LDS per workgroup");
+  // Key rows: chunk c of key r at c ^ (r mod CH), so that the 16 keys of a
+  // score operand read distinct banks. Value rows: 32-byte pair j of key r at
+  // pair (j + rot(r)) mod NPR, rot(r) = (r mod 8) >> (3 - t) with 2^t the
+  // largest power of two (at most 8) dividing NPR: the transposed reads of 8
+  // consecutive keys fall in distinct 8-bank groups.
+  static constexpr int NPR = VCH / 2;
+  static constexpr int ROT_SHIFT = NPR % 8 == 0 ? 0 : NPR % 4 == 0 ? 1 : NPR % 2 == 0 ? 2 : 3;
+  __device__ __forceinline__ static int swz_k(int r) { return r & (CH < 16 ? CH - 1 : 15); }
+  __device__ __forceinline__ static int rot_v(int r) { return (r & 7) >> ROT_SHIFT; }
+  __device__ __forceinline__ static int vchunk_lds(int r, int c) {
+    return 2 * (((c >> 1) + rot_v(r)) % NPR) + (c & 1);
+  }
+  __device__ __forceinline__ static int vchunk_src(int r, int c) {
+    return 2 * (((c >> 1) + NPR - rot_v(r)) % NPR) + (c & 1);
+  }
+
+  // Loads of a block: NL of 64 lanes x 16 bytes, load j filling slot uint4s
+  // 64j .. 64j + 63 (keys for j < KSLOT / 64, then values); wave w issues
+  // loads w * LPW .. + LPW - 1. Lane byte offsets count from the block's
+  // first row (below 2^31: the host bounds 32 * stride). Block i's rows end
+  // at kmax, so keys no column of the workgroup sees read as zeros whatever
+  // the memory holds; blocks past nblk - 1 read nothing. (Member functions
+  // rather than lambdas in the kernel: a lambda there that makes buffer
+  // resources cost the kernel its host stub.)
+  struct Loads {
+    const T* kb;
+    const T* vb;
+    int64_t ks2, vs2, kmax, nblk;
+    uint32_t loff[LPW];
+    bool lkey[LPW];
+    __device__ __forceinline__ void init(const SdpaArgs& p, int64_t b, int64_t kvh, int64_t kmax_,
+                                         int64_t nblk_, int wave, int lane) {
+      constexpr uint32_t E = sizeof(T);
+      kb = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
+      vb = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
+      ks2 = p.ks[2];
+      vs2 = p.vs[2];
+      kmax = kmax_;
+      nblk = nblk_;
+#pragma unroll
+      for (int u = 0; u < LPW; u++) {
+        const int j = wave * LPW + u;
+        lkey[u] = j < KSLOT / 64;
+        if (lkey[u]) {
+          const int pos = j * 64 + lane, r = pos / CH, c = (pos % CH) ^ swz_k(r);
+          loff[u] = (uint32_t)((r * ks2 + c * 8) * E);
+        } else {
+          const int pos = (j - KSLOT / 64) * 64 + lane, r = pos / VCH, c = vchunk_src(r, pos % VCH);
+          loff[u] = (uint32_t)((r * vs2 + c * 8) * E);
+        }
+      }
+    }
+    // This wave's loads of block i into the slot at dst (the slot's first
+    // uint4 plus this wave's first load).
+    __device__ __forceinline__ void issue(int64_t i, uint4* dst) const {
+      const int64_t key0 = i * kBlk;
+      const bool in = i < nblk;
+      const auto rk = make_rsrc(kb + (in ? key0 * ks2 : 0),
+                                in ? ((kmax - key0 - 1) * ks2 + D) * (int64_t)sizeof(T) : 0);
+      const auto rv = make_rsrc(vb + (in ? key0 * vs2 : 0),
+                                in ? ((kmax - key0 - 1) * vs2 + V) * (int64_t)sizeof(T) : 0);
+#pragma unroll
+      for (int u = 0; u < LPW; u++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(lkey[u] ? rk : rv, (lds_void_t*)(dst + u * 64),
+                                                 16, (int)loff[u], 0, 0, 0);
+    }
+  };
+};
+
+template <typename T, int D, int V, int NW, int GP>
+__global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
+  using C = Shared<T, D, V, NW, GP>;
+  constexpr int NQ = C::NQ, NB = C::NB, CH = C::CH, VCH = C::VCH, LPW = C::LPW;
+  constexpr int COLS = 16 * NW;  // columns per workgroup
+  __shared__ uint4 ring[C::S * C::SLOT];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r16 = lane & 15;
+
+  // Workgroup -> (batch, kv head, block of COLS of the G x qL columns of that
+  // kv head -- column cc is row cc / G, head cc % G).
+  const int64_t G = p.H / p.Hkv;
+  const int64_t ncol = G * p.qL;
+  const int64_t ncb = (ncol + COLS - 1) / COLS;
+  int64_t t = xcd_remap(blockIdx.x, (int)(p.B * p.Hkv * ncb));
+  // Causal: the last column blocks see the most keys; they start first.
+  const int64_t cb = p.mask_mode == BI_MASK_CAUSAL ? ncb - 1 - t % ncb : t % ncb;
+  t /= ncb;
+  const int64_t kvh = t % p.Hkv;
+  const int64_t b = t / p.Hkv;
+  const int64_t c0 = cb * COLS;
+
+  auto kend_of = [&](int64_t s) __attribute__((always_inline)) -> int64_t {
+    if (p.mask_mode != BI_MASK_CAUSAL) return p.N;
+    const int64_t last = s + p.causal_offset;
+    return last < 0 ? 0 : (last + 1 < p.N ? last + 1 : p.N);
+  };
+  const int64_t last_cc = (c0 + COLS < ncol ? c0 + COLS : ncol) - 1;
+  const int64_t kmax = kend_of(last_cc / G);  // keys some column of the workgroup sees
+  const int64_t nblk = (kmax + kBlk - 1) / kBlk;
+  // This wave's columns w0 .. w0 + 15: the keys the last of them sees, and
+  // those every one of them sees.
+  const int64_t w0 = c0 + 16 * wave;
+  const bool wany = w0 < ncol;
+  const int64_t wlast = (w0 + 16 < ncol ? w0 + 16 : ncol) - 1;
+  const int64_t kmax_w = wany ? kend_of(wlast / G) : 0;
+  const int64_t kfull_w = wany ? kend_of(w0 / G) : 0;
+
+  // This lane's column, its query as the B operand of the score MFMAs
+  // (Q[col][32i + 8g ..]), and the 4 chains' state.
+  const int64_t cc = w0 + r16;
+  const bool colv = cc < ncol;
+  const int64_t srow = colv ? cc / G : 0;
+  const int64_t head = kvh * G + (colv ? cc % G : 0);
+  const int kend = colv ? (int)kend_of(srow) : 0;
+  uint4 qt[NQ];
+  {
+    const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + head * p.qs[1] + srow * p.qs[2];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) qt[i] = colv ? ld16(qrow + 32 * i + 8 * g) : make_uint4(0, 0, 0, 0);
+  }
+  float m[4], l[4];
+  f32x4_t o[4][NB];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    m[c] = -FLT_MAX;
+    l[c] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NB; i++) o[c][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  typename C::Loads ld;
+  ld.init(p, b, kvh, kmax, nblk, wave, lane);
+  // Block i of group half h (0 or 1) into slot h * GP + i mod GP.
+  auto issue = [&](int64_t i, int slot) __attribute__((always_inline)) {
+    ld.issue(i, ring + slot * C::SLOT + wave * LPW * 64);
+  };
+
+  // LDS lane addresses in slot 0 of each group: lane (r16, g) reads chunk
+  // 4i + g of key r16 as the A operand of the score MFMAs (key 16 + r16:
+  // + 16 rows, the same swizzle); lane r16 of group g addresses value key
+  // 4g + r16 / 4 at dim 16db + 4 (r16 mod 4) for the transposed reads (key
+  // + 16: + 16 rows). Slots within a group and key halves are constant
+  // offsets. The empty asm keeps each an opaque register, so the unrolled
+  // reads do not each recompute theirs.
+  constexpr int NBASE = C::TWO_BASES ? 2 : 1;
+  uint32_t kofs[NBASE][NQ], vofs[NBASE][NB];
+  {
+    const uint32_t rb = (uint32_t)(uintptr_t)(lds_void_t*)ring;
+    const int kr = 4 * g + (r16 >> 2);
+#pragma unroll
+    for (int h = 0; h < NBASE; h++) {
+#pragma unroll
+      for (int i = 0; i < NQ; i++) {
+        kofs[h][i] = rb + h * C::HALF + (r16 * CH + ((4 * i + g) ^ C::swz_k(r16))) * 16;
+        asm volatile("" : "+v"(kofs[h][i]));
+      }
+#pragma unroll
+      for (int db = 0; db < NB; db++) {
+        const int col = 16 * db + 4 * (r16 & 3);
+        vofs[h][db] = rb + h * C::HALF + C::KSLOT * 16 +
+                      (kr * VCH + C::vchunk_lds(kr, col >> 3)) * 16 + (col & 7) * 2;
+        asm volatile("" : "+v"(vofs[h][db]));
+      }
+    }
+  }
+
+  // One block of chain c from slot `slot` (its loads have landed for every
+  // wave: the caller waited and synchronised).
+  auto compute = [&](auto slot_c, auto chain, int64_t blk) __attribute__((always_inline)) {
+    constexpr int c = decltype(chain)::value;
+    constexpr int slot = decltype(slot_c)::value;
+    constexpr int h = C::TWO_BASES ? slot / GP : 0;
+    constexpr int SOFF = (slot - h * GP) * C::SLOT * 16;
+    // Scores: S^T tiles (16 keys x 16 columns); lane (g, r16) holds keys
+    // 16kt + 4g + e of column r16.
+    f32x4_t sc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+      u32x4_t kl[NQ];
+#pragma unroll
+      for (int i = 0; i < NQ; i++) kl[i] = ds_read_b128_at(kofs[h][i], SOFF + kt * 16 * CH * 16);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < NQ; i++) asm volatile("" : "+v"(kl[i]));
+      sc[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < NQ; i++)
+        sc[kt] = mma32(T(0), __builtin_bit_cast(uint4, kl[i]), qt[i], sc[kt]);
+    }
+    // V^T blocks (dims 16db .., keys 16kt + 4g ..): lane r16 receives
+    // V[16kt + 4g + t][16db + r16]. Read before the softmax, which hides
+    // their latency.
+    u32x2_t va[NB][2];
+#pragma unroll
+    for (int db = 0; db < NB; db++)
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+        va[db][kt] = ds_read_tr_at(vofs[h][db], SOFF + kt * 16 * VCH * 16);
+    // Softmax of chain c over the block (the per-column steps of
+    // sdpa_mfma_kernel, in the same order).
+    const int key0 = (int)blk * kBlk + 4 * g;
+    uint2 ph[2], pl[2];
+    float f;
+    auto softmax = [&](auto full_tag) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      float s[2][4];
+      bool use[2][4];
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          s[kt][e] = sc[kt][e] * p.scale2;
+          use[kt][e] = FULL || key0 + 16 * kt + e < kend;
+        }
+      float bm = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
+      bm = col_max(bm);
+      const bool any = bm > -INFINITY;
+      const float mn = (any && bm > m[c] + 8.f) ? bm : m[c];
+      f = mn == m[c] ? 1.f : __builtin_amdgcn_exp2f(m[c] - mn);
+      float pv[2][4];
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(s[kt][e] - mn) : 0.f;
+          ps = ps + pv[kt][e];
+        }
+      ps = col_sum(ps);
+      l[c] = __builtin_fmaf(l[c], f, ps);
+      m[c] = mn;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) split_p<T>(pv[kt], ph[kt], pl[kt]);
+    };
+    if ((blk + 1) * kBlk <= kfull_w)
+      softmax(std::true_type{});
+    else
+      softmax(std::false_type{});
+    // Rescale (+0.0: o is never -0.0).
+    if (f != 1.f) {
+#pragma unroll
+      for (int i = 0; i < NB; i++) o[c][i] = o[c][i] * f + 0.f;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int db = 0; db < NB; db++) asm volatile("" : "+v"(va[db][0]), "+v"(va[db][1]));
+    // o += P . V over the block's 32 keys, hi plane then lo plane.
+#pragma unroll
+    for (int db = 0; db < NB; db++) {
+      const uint4 vt =
+          join(__builtin_bit_cast(uint2, va[db][0]), __builtin_bit_cast(uint2, va[db][1]));
+      o[c][db] = mma32(T(0), vt, join(ph[0], ph[1]), o[c][db]);
+      o[c][db] = mma32(T(0), vt, join(pl[0], pl[1]), o[c][db]);
+    }
+  };
+
+  // Group q holds blocks q * GP .. + GP - 1 in slots (q mod 2) * GP ..;
+  // group q + 1 loads while group q is computed. A wave skips a block none
+  // of its columns can see (for them it changes nothing). Unrolled over UG
+  // groups (UG * GP a multiple of 4, UG even), so slot and chain indices are
+  // compile-time.
+  constexpr int UG = GP >= 4 ? 2 : 4 / GP;
+#pragma unroll
+  for (int u = 0; u < GP; u++) issue(u, u);
+  int64_t q0 = 0;
+  auto group = [&](auto qc) __attribute__((always_inline)) -> bool {
+    constexpr int uq = decltype(qc)::value;
+    const int64_t q = q0 + uq;
+    if (q * GP >= nblk) return false;  // the same for every wave
+    // This wave's loads are group q's; after the barrier, every wave's are,
+    // and every wave has finished group q - 1.
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < GP; u++) issue((q + 1) * GP + u, ((uq + 1) % 2) * GP + u);
+    auto blockstep = [&](auto bc) __attribute__((always_inline)) -> bool {
+      constexpr int u = decltype(bc)::value;
+      const int64_t i = q * GP + u;
+      if (i >= nblk) return false;
+      if (i * kBlk < kmax_w)
+        compute(std::integral_constant<int, (uq % 2) * GP + u>{},
+                std::integral_constant<int, (uq * GP + u) % 4>{}, i);
+      return true;
+    };
+    static_for<0, GP>(blockstep);
+    return true;
+  };
+  for (; q0 * GP < nblk; q0 += UG) static_for<0, UG>(group);
+  // The loads issued past the last block (they read nothing but still write
+  // their slots) complete before the workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+
+  // Merge the 4 chains in order, in registers (the sink first: -FLT_MAX
+  // without one).
+  const float sk = p.sinks ? (float)static_cast<const T*>(p.sinks)[head] * kLog2e : -FLT_MAX;
+  float M = sk;
+#pragma unroll
+  for (int c = 0; c < 4; c++) M = fmaxf(M, m[c]);
+  float L = p.sinks ? __builtin_amdgcn_exp2f(sk - M) : 0.f;  // the sink's l = 1
+  float ec[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    ec[c] = __builtin_amdgcn_exp2f(m[c] - M);
+    L = __builtin_fmaf(l[c], ec[c], L);
+  }
+  T* __restrict__ out = static_cast<T*>(p.out) + ((b * p.H + head) * p.qL + srow) * V;
+#pragma unroll
+  for (int db = 0; db < NB; db++) {
+    f32x4_t O = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) O[e] = __builtin_fmaf(o[c][db][e], ec[c], O[e]);
+    unsigned short ob[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) ob[e] = tbits((T)(L == 0.f ? O[e] : O[e] / L));
+    if (colv)
+      *reinterpret_cast<uint2*>(out + 16 * db + 4 * g) =
+          make_uint2(ob[0] | ((uint32_t)ob[1] << 16), ob[2] | ((uint32_t)ob[3] << 16));
+  }
+}
+
 // Kernel of launch shape `SHAPE` (SdpaShape) for head dims (D, V). The rows
 // shape with an array mask loads the mask values at the start of their own
 // block and no keys ahead, which keeps two workgroups per CU within the
@@ -750,7 +1133,12 @@ constexpr SdpaKernelFn mfma_kernel() {
   constexpr int MK = MASK ? 1 : 0;
   constexpr int PK = sdpa_wide(D, V) ? 0 : 1;
   constexpr int WS = sdpa_shape_splits(V, SHAPE);
-  if constexpr (SHAPE == SDPA_ROWS) {
+  if constexpr (SHAPE == SDPA_SHARED) {
+    if constexpr (sdpa_shared_dims(D, V) && !MASK)
+      return sdpa_shared_kernel<T, D, V, sdpa_shared_waves(D, V), 2>;
+    else
+      return nullptr;
+  } else if constexpr (SHAPE == SDPA_ROWS) {
     return sdpa_mfma_kernel<T, D, V, sdpa_rows_tiles(D, V), MASK ? 0 : PK, 2, WS, MASK ? 2 : 0,
                             false>;
   } else if constexpr (SHAPE == SDPA_TILE) {
@@ -769,6 +1157,7 @@ SdpaKernelFn mfma_kernel_shape(int shape) {
     case SDPA_SPLIT2: return mfma_kernel<T, D, V, MASK, SDPA_SPLIT2>();
     case SDPA_SPLIT4: return mfma_kernel<T, D, V, MASK, SDPA_SPLIT4>();
     case SDPA_SPLIT8: return mfma_kernel<T, D, V, MASK, SDPA_SPLIT8>();
+    case SDPA_SHARED: return mfma_kernel<T, D, V, MASK, SDPA_SHARED>();
   }
   return nullptr;
 }

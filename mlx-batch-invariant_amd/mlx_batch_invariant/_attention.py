@@ -123,12 +123,14 @@ def _sdpa_eager(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks,
     return out
 
 
-def launch_shape(q, k, v):
-    """The launch shape bi_sdpa picks for these operands (include/bi_testing.h):
-    _lib.SDPA_ROWS ... for bf16/f16, log2(query heads per workgroup) for fp32."""
+def launch_shape(q, k, v, mask_mode=_lib.MASK_NONE):
+    """The launch shape bi_sdpa picks for these operands and mask mode
+    (include/bi_testing.h): _lib.SDPA_ROWS ... for bf16/f16, log2(query heads
+    per workgroup) for fp32."""
     B, H, qL, D = q.shape
     L = _lib.lib()
-    rc = L.bi_sdpa_pick_shape(B, H, k.shape[1], qL, D, v.shape[-1], _lib.DTYPE_CODES[q.dtype], 0)
+    rc = L.bi_sdpa_pick_shape(B, H, k.shape[1], qL, D, v.shape[-1], _lib.DTYPE_CODES[q.dtype],
+                              int(mask_mode), 0)
     if rc < 0:
         _lib.check(rc, "bi_sdpa_pick_shape")
     return rc

@@ -49,7 +49,7 @@ SIGNATURES = {
     "bi_qgemm_with_geometry": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                         _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "bi_sdpa_pick_shape": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
-                                    _c_int]),
+                                    _c_int, _c_int]),
     "bi_sdpa_shape_info": (_c_int, [_c_i64, _c_i64, _c_int, _c_int, ctypes.POINTER(_c_int),
                                     ctypes.POINTER(_c_int)]),
     "bi_sdpa_with_shape": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64p, _c_vp, _c_vp,
@@ -59,7 +59,8 @@ SIGNATURES = {
 }
 
 # Attention launch shapes (include/bi_testing.h): bf16 / f16 on matrix cores.
-SDPA_ROWS, SDPA_TILE, SDPA_SPLIT2, SDPA_SPLIT4, SDPA_SPLIT8 = 0, 1, 2, 3, 4
+SDPA_ROWS, SDPA_TILE, SDPA_SPLIT2, SDPA_SPLIT4, SDPA_SPLIT8, SDPA_SHARED = 0, 1, 2, 3, 4, 5
+SDPA_NUM_SHAPES = 6
 
 ABI_VERSION = 1
 

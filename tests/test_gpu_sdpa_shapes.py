@@ -1,18 +1,20 @@
 """GPU parity tests of the attention launch shapes and head dims.
 
 bi_sdpa picks a launch shape from the grid (include/bi_testing.h): for
-bf16/f16 the prefill "rows" shape (several 16-column tiles per workgroup), one
-tile, or one tile with the output dims split over 2/4/8 workgroups; for fp32
-how many query heads share a workgroup's loads. The reference has a single
+bf16/f16 the prefill "rows" shape (several 16-column tiles per workgroup), the
+prefill "shared" shape (one column tile per wave, every key block loaded once
+for all waves), one tile, or one tile with the output dims split over 2/4/8
+workgroups; for fp32 how many query heads share a workgroup's loads. The reference has a single
 launch shape (_attention.py:241-250) and rejects any route switch on query
 length (reference ROADMAP.md:91-94), so every shape must give the same bits:
 
   * every shape, forced through bi_sdpa_with_shape, gives identical bits on the
     same input, for every built (D, V) pair, element type and mask mode;
-  * the prefill rows shape, selected by bi_sdpa itself at the shapes it is
-    built for, gives each row the bits of that row computed alone at query
-    length 1 over its visible keys (a one-tile shape), and is accurate against
-    the float64 oracle (reference tests/test_invariance.py:408-432);
+  * the prefill rows and shared shapes, selected by bi_sdpa itself at the
+    shapes they are built for, give each row the bits of that row computed
+    alone at query length 1 over its visible keys (a one-tile shape), are
+    accurate against the float64 oracle (reference
+    tests/test_invariance.py:408-432), and give each other's bits;
   * keys no query row can see (an unwritten cache tail) never reach the
     output, whatever they hold (reference _attention.py:92-98).
 """
@@ -61,7 +63,7 @@ def shapes_for(dtype, D, V, G):
     L = _lib.lib()
     code = _lib.DTYPE_CODES[dtype]
     out = []
-    for s in range(5):
+    for s in range(_lib.SDPA_NUM_SHAPES):
         c, w = ctypes.c_int(), ctypes.c_int()
         if L.bi_sdpa_shape_info(D, V, code, s, c, w) != _lib.OK:
             continue
@@ -99,6 +101,9 @@ def test_every_shape_gives_the_same_bits(cuda, D, V):
                                 ("bool", keep, None), ("sinks", None, sinks)):
             ref = None
             for s in shapes:
+                if s == _lib.SDPA_SHARED and label in ("additive", "bool"):
+                    # Built without array masks: bi_sdpa never picks it for one.
+                    continue
                 y = run(q, k, v, spec, shape=s, sinks=sk)
                 got = bits(y)
                 if ref is None:
@@ -153,29 +158,40 @@ ROWS_CASES = [(4, 64), (1, 513), (2, 513), (1, 2048), (2, 2048)]
 @pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("dname,dtype", LOW)
 def test_prefill_rows_shape_is_invariant_and_accurate(cuda, dname, dtype, D):
-    """The prefill "rows" shape at 32/8 heads: bi_sdpa selects it for these
-    problems; rows 0, middle and last are bitwise equal to the same row computed
-    alone at query length 1 (which takes a one-tile shape), and every head of
-    those rows is within the reference's float64 bound and no worse than 4x the
-    reference-order fp32 restatement (tests:408-432). Masks: end-aligned
-    causal (mask="causal"), start-aligned causal (torch is_causal), additive
-    per row, boolean per row."""
+    """The prefill shapes at 32/8 heads: bi_sdpa selects "rows" or (D = 128
+    without an array mask, on the larger grids) "shared" for these problems;
+    rows 0, middle and last are bitwise equal to the same row computed alone at
+    query length 1 (which takes a one-tile shape), and every head of those rows
+    is within the reference's float64 bound and no worse than 4x the
+    reference-order fp32 restatement (tests:408-432). Where "shared" is built
+    (D <= 128, no array mask), it and "rows", forced, give the whole output the
+    same bits. Masks: end-aligned causal (mask="causal"), start-aligned causal
+    (torch is_causal), additive per row, boolean per row."""
     H, Hkv = 32, 8
+    picked = set()
     for B, qL in ROWS_CASES:
         for N in (qL, 4200):
             seed = 1000 * B + qL + N + D
             q = rn((B, H, qL, D), dtype, seed, device=cuda)
             k = rn((B, Hkv, N, D), dtype, seed + 1, device=cuda)
             v = rn((B, Hkv, N, D), dtype, seed + 2, device=cuda)
-            assert _attention.launch_shape(q, k, v) == _lib.SDPA_ROWS, (B, qL, D)
             add, keep = _masks(B, qL, N, dtype, cuda, seed + 3)
             rows = sorted({0, qL // 2, qL - 1})
             b = B - 1
             for label, spec in (("end", "end"), ("start", "start"), ("additive", add),
                                 ("bool", keep)):
+                mode = _mask_mode(spec, q, k)[0]
+                shape = _attention.launch_shape(q, k, v, mode)
+                assert shape in (_lib.SDPA_ROWS, _lib.SDPA_SHARED), (B, qL, D, label, shape)
+                picked.add(shape)
                 y = run(q, k, v, spec)
-                case = "%s D=%d B=%d qL=%d N=%d %s" % (dname, D, B, qL, N, label)
+                case = "%s D=%d B=%d qL=%d N=%d %s shape %d" % (dname, D, B, qL, N, label, shape)
                 assert torch.isfinite(y).all(), case
+                if D <= 128 and mode != _lib.MASK_ARRAY:
+                    for forced in (_lib.SDPA_ROWS, _lib.SDPA_SHARED):
+                        yf = run(q, k, v, spec, shape=forced)
+                        d = int((bits(yf) != bits(y)).sum())
+                        assert d == 0, "%s: forced shape %d: %d differ" % (case, forced, d)
                 for s in rows:
                     alone = _alone(q, k, v, spec, b, s)
                     assert np.array_equal(bits(alone[0, :, 0]), bits(y[b, :, s])), (case, s)
@@ -186,6 +202,10 @@ def test_prefill_rows_shape_is_invariant_and_accurate(cuda, dname, dtype, D):
                 err_fixed = np.abs(fixed - want).max() / scale
                 assert err < TOL[dname], "%s: %.3e" % (case, err)
                 assert err < 4 * err_fixed + 1e-7, "%s: %.3e vs %.3e" % (case, err, err_fixed)
+    # bi_sdpa's own choice covers the rows shape everywhere, and the shared
+    # shape at D = 128.
+    assert _lib.SDPA_ROWS in picked
+    assert (_lib.SDPA_SHARED in picked) == (D == 128), picked
 
 
 @pytest.mark.parametrize("dname,dtype", LOW + [("float32", torch.float32)])

@@ -122,7 +122,7 @@ def test_sdpa_shape_abi_without_a_gpu():
                                     0.1, 0, 0, dtype, shape, None)
 
     assert forced(-1) == _lib.EINVAL
-    assert forced(5) == _lib.EINVAL and "shape" in _err()
+    assert forced(_lib.SDPA_NUM_SHAPES) == _lib.EINVAL and "shape" in _err()
     assert forced(3, dtype=_lib.F32) == _lib.EINVAL      # 8 heads per workgroup: D <= 64 only
     assert forced(2, dtype=_lib.F32, H=8, Hkv=4) == _lib.EINVAL  # 4 heads do not divide 2
     assert forced(0, D=96, V=64) == _lib.EUNSUPPORTED
@@ -141,7 +141,12 @@ def test_sdpa_shape_abi_without_a_gpu():
     assert info(96, 96, _lib.SDPA_SPLIT8) == (16, 2)     # 96 = 6 x 16 dims: splits in two
     assert info(192, 192, _lib.SDPA_SPLIT8) == (16, 4)
     assert info(32, 32, _lib.SDPA_SPLIT4) == (16, 2)
-    assert info(128, 128, 5) == _lib.EINVAL
+    assert info(128, 128, _lib.SDPA_SHARED) == (128, 1)  # 8 waves, one column tile each
+    assert info(64, 64, _lib.SDPA_SHARED) == (128, 1)
+    assert info(32, 32, _lib.SDPA_SHARED) == (64, 1)     # 4 loads per key block: 4 waves
+    assert info(96, 96, _lib.SDPA_SHARED) == _lib.EINVAL
+    assert info(256, 256, _lib.SDPA_SHARED) == _lib.EINVAL
+    assert info(128, 128, _lib.SDPA_NUM_SHAPES) == _lib.EINVAL
     assert info(64, 64, 3, _lib.F32) == (8, 1)
     assert info(128, 128, 3, _lib.F32) == _lib.EINVAL
     assert info(256, 256, 1, _lib.F32) == (2, 1)
@@ -153,8 +158,8 @@ def test_sdpa_shape_policy():
     GPU tests prove by forcing each one)."""
     L = _lib.lib()
 
-    def pick(B, qL, H=32, Hkv=8, D=128, V=128, dtype=_lib.BF16):
-        return L.bi_sdpa_pick_shape(B, H, Hkv, qL, D, V, dtype, 256)
+    def pick(B, qL, H=32, Hkv=8, D=128, V=128, dtype=_lib.BF16, mask=_lib.MASK_NONE):
+        return L.bi_sdpa_pick_shape(B, H, Hkv, qL, D, V, dtype, mask, 256)
 
     assert pick(64, 1) == pick(32, 1) == _lib.SDPA_TILE  # configs[2] decode, B >= 32
     assert pick(16, 1) == _lib.SDPA_SPLIT2
@@ -163,8 +168,13 @@ def test_sdpa_shape_policy():
     assert pick(1, 16) == _lib.SDPA_SPLIT8      # configs[3] chunk of 16 query rows
     assert pick(1, 64) == _lib.SDPA_SPLIT2      # 8 streams x 16 tiles: too few for rows
     assert pick(4, 64) == pick(1, 256) == _lib.SDPA_ROWS  # prefill: rows fill 256 CUs
-    assert pick(1, 2048) == pick(2, 513) == _lib.SDPA_ROWS
+    assert pick(2, 513) == _lib.SDPA_ROWS       # 272 shared workgroups: under 2 per CU
+    assert pick(1, 2048) == pick(4, 1024) == _lib.SDPA_SHARED  # D = V = 128, no array mask
+    assert pick(1, 2048, mask=_lib.MASK_CAUSAL) == _lib.SDPA_SHARED
+    assert pick(1, 2048, mask=_lib.MASK_ARRAY) == _lib.SDPA_ROWS
+    assert pick(1, 2048, D=64, V=64) == _lib.SDPA_ROWS
     assert pick(1, 2048, D=256, V=256) == _lib.SDPA_ROWS
+    assert pick(1, 2048, mask=7) == _lib.EINVAL
     assert pick(64, 1, dtype=_lib.F32) == 2     # fp32: four query heads per workgroup
     assert pick(1, 2048, dtype=_lib.F32) == 1   # fp32 prefill: two
     assert pick(1, 1, dtype=_lib.F32) == 0
