@@ -250,6 +250,10 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy three times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--prefill-shape", choices=("rows", "shared"),
+                    help="only run the causal prefill (B=1, 32/8 heads, L=2048, D=128, bf16) "
+                         "five times through one forced attention launch shape (for counter "
+                         "passes of one kernel)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the invariant GEMM and attention have no "
@@ -272,6 +276,19 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "copy", "bytes": src.numel() * 4}))
+        return
+    if args.prefill_shape:
+        from mlx_batch_invariant import _attention, _lib
+        shape = {"rows": _lib.SDPA_ROWS, "shared": _lib.SDPA_SHARED}[args.prefill_shape]
+        g = torch.Generator().manual_seed(0)
+        L, D = 2048, SDPA["D"]
+        q, k, v = (torch.randn(1, h, L, D, generator=g).to(torch.bfloat16).to(dev)
+                   for h in (SDPA["H"], SDPA["Hkv"], SDPA["Hkv"]))
+        for _ in range(5):
+            _attention._sdpa_eager(q, k, v, 1.0 / math.sqrt(D), _lib.MASK_CAUSAL, None,
+                                   (0, 0, 0), 0, None, shape)
+        torch.cuda.synchronize()
+        print(json.dumps({"prefill_shape": args.prefill_shape, "launches": 5}))
         return
     ops = make_inputs(torch, dev)
     step_flops = sum(gemm_flops(M, K, N) for K, N in SHAPES)
