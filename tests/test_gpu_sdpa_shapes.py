@@ -214,32 +214,38 @@ def test_unwritten_cache_tail_never_reaches_the_output(cuda, dname, dtype):
     the output is finite and bitwise equal to the same call with a zero tail,
     for start-aligned causal (torch is_causal over a longer cache) and for a
     cache view k[:, :, :N] whose storage continues with NaN rows (mask="causal",
-    aligned to the end of the view), at decode and prefill shapes."""
+    aligned to the end of the view), at decode and prefill shapes: the one
+    bi_sdpa picks, and the two prefill shapes forced (bf16/f16)."""
     H, Hkv, D, NP = 32, 8, 128, 1200
     for B, qL in ((1, 1), (3, 5), (1, 300), (2, 700)):
         q = rn((B, H, qL, D), dtype, 111, device=cuda)
         k = rn((B, Hkv, NP, D), dtype, 112, device=cuda)
         v = rn((B, Hkv, NP, D), dtype, 113, device=cuda)
-        # Start-aligned: row s sees keys 0..s; keys from qL on are never read.
-        kn, vn, kz, vz = k.clone(), v.clone(), k.clone(), v.clone()
-        kn[:, :, qL:] = float("nan")
-        vn[:, :, qL:] = float("nan")
-        kz[:, :, qL:] = 0
-        vz[:, :, qL:] = 0
-        got, want = run(q, kn, vn, "start"), run(q, kz, vz, "start")
-        assert torch.isfinite(got).all(), (dname, B, qL)
-        assert np.array_equal(bits(got), bits(want)), (dname, B, qL)
-        # End-aligned over a view of the first N rows; storage past N is NaN.
-        N = NP - 77
-        kn, vn, kz, vz = k.clone(), v.clone(), k.clone(), v.clone()
-        kn[:, :, N:] = float("nan")
-        vn[:, :, N:] = float("nan")
-        kz[:, :, N:] = 0
-        vz[:, :, N:] = 0
-        got = run(q, kn[:, :, :N], vn[:, :, :N], "end")
-        want = run(q, kz[:, :, :N], vz[:, :, :N], "end")
-        assert torch.isfinite(got).all(), (dname, B, qL)
-        assert np.array_equal(bits(got), bits(want)), (dname, B, qL)
+        shapes = [None]
+        if dtype != torch.float32 and qL > 16:
+            shapes += [_lib.SDPA_ROWS, _lib.SDPA_SHARED]
+        for shape in shapes:
+            case = (dname, B, qL, shape)
+            # Start-aligned: row s sees keys 0..s; keys from qL on are never read.
+            kn, vn, kz, vz = k.clone(), v.clone(), k.clone(), v.clone()
+            kn[:, :, qL:] = float("nan")
+            vn[:, :, qL:] = float("nan")
+            kz[:, :, qL:] = 0
+            vz[:, :, qL:] = 0
+            got, want = run(q, kn, vn, "start", shape), run(q, kz, vz, "start", shape)
+            assert torch.isfinite(got).all(), case
+            assert np.array_equal(bits(got), bits(want)), case
+            # End-aligned over a view of the first N rows; storage past N is NaN.
+            N = NP - 77
+            kn, vn, kz, vz = k.clone(), v.clone(), k.clone(), v.clone()
+            kn[:, :, N:] = float("nan")
+            vn[:, :, N:] = float("nan")
+            kz[:, :, N:] = 0
+            vz[:, :, N:] = 0
+            got = run(q, kn[:, :, :N], vn[:, :, :N], "end", shape)
+            want = run(q, kz[:, :, :N], vz[:, :, :N], "end", shape)
+            assert torch.isfinite(got).all(), case
+            assert np.array_equal(bits(got), bits(want)), case
 
 
 @pytest.mark.parametrize("D,V", PAIRS)
