@@ -528,7 +528,8 @@ int sdpa_run(const void* q, const void* k, const void* v, const void* mask,
   if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_sdpa: grid too large");
   if (!fn)
     return bi::fail(BI_EINVAL, "bi_sdpa: launch shape %d is not built for this mask", shape);
-  const int threads = dtype == BI_F32 ? kThreads : sdpa_shape_threads(D, V, shape);
+  const int threads =
+      dtype == BI_F32 ? kThreads : sdpa_shape_threads(D, V, shape, mask_mode == BI_MASK_ARRAY);
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(threads), 0,
                      static_cast<hipStream_t>(hip_stream), p);
   const hipError_t e = hipGetLastError();

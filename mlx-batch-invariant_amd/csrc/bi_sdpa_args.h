@@ -36,7 +36,8 @@ typedef void (*SdpaKernelFn)(SdpaArgs);
 //   SDPA_TILE    one column tile, output dims whole (or split in two for V > 128)
 //   SDPA_SPLITn  one column tile, output dims split over n workgroups (decode),
 //                capped by the largest power of two that leaves each workgroup
-//                a multiple of 16 dims
+//                a multiple of 16 dims; for D = V = 128 without an array mask,
+//                4 more waves only issue the chains' loads
 //   SDPA_SHARED  one 16-column tile per wave, every wave walking every key
 //                block with all 4 chains' state of its columns: a key and value
 //                block is loaded once into LDS for 4-8 column tiles (prefill;
@@ -70,9 +71,17 @@ constexpr int sdpa_shape_columns(int64_t D, int64_t V, int shape) {
          : shape == SDPA_SHARED ? 16 * sdpa_shared_waves(D, V)
                                 : 16;
 }
-// Threads per workgroup: 4 waves (one per chain), or one per column tile.
-constexpr int sdpa_shape_threads(int64_t D, int64_t V, int shape) {
-  return shape == SDPA_SHARED ? 64 * sdpa_shared_waves(D, V) : 256;
+// The dim-split shapes for D = V = 128 without an array mask stage keys and
+// values in LDS through loader waves, one beside each chain's wave.
+constexpr bool sdpa_loaders(int64_t D, int64_t V, int shape, bool array_mask) {
+  return !array_mask && D == 128 && V == 128 && shape >= SDPA_SPLIT2 && shape <= SDPA_SPLIT8;
+}
+// Threads per workgroup: 4 waves (one per chain), 8 with loader waves, or
+// one wave per column tile.
+constexpr int sdpa_shape_threads(int64_t D, int64_t V, int shape, bool array_mask) {
+  return shape == SDPA_SHARED                        ? 64 * sdpa_shared_waves(D, V)
+         : sdpa_loaders(D, V, shape, array_mask) ? 512
+                                                     : 256;
 }
 
 // The MFMA kernel of one head-dim pair for (dtype, array mask or not, shape);

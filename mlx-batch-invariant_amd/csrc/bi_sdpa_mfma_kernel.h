@@ -399,8 +399,12 @@ struct Chain {
   }
 };
 
-template <typename T, int D, int V, int CT, int PK, int SV, int WS, int MK, bool KL>
-__global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
+// LW: 0, or kWaves loader waves (keys in LDS only). A loader wave issues the
+// loads of one chain's blocks, so the chain wave's instruction stream holds
+// no load issue (which stalls while the memory pipeline is busy).
+template <typename T, int D, int V, int CT, int PK, int SV, int WS, int MK, bool KL, int LW>
+__global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs p) {
+  static_assert(LW == 0 || (LW == kWaves && KL && PK == 0), "loader waves: one per chain");
   using C = Chain<T, D, V, CT, PK, SV, WS, MK, KL>;
   constexpr int NQ = C::NQ, NB = C::NB, VCH = C::VCH;
   constexpr int COLS = 16 * CT;  // columns per workgroup
@@ -415,7 +419,9 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // the chain
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool loader = LW != 0 && wv >= kWaves;  // wave kWaves + c loads chain c's blocks
+  const int wave = loader ? wv - kWaves : wv;   // the chain
   const int g = lane >> 4, r16 = lane & 15;
 
   // Workgroup -> (batch, kv head, block of COLS of the G x qL columns of that
@@ -480,6 +486,37 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   const int wslot = wave * C::VSLOT;  // this wave's slot within each array
   C ld;
   ld.init(p, b, kvh, ws, wave, nit, lane, mrow, kmax);
+  // With loader waves every wave runs chain 0's number of steps (the most),
+  // one barrier per step.
+  const int64_t nit0 = nblk > 0 ? (nblk + kWaves - 1) / kWaves : 0;
+  if constexpr (LW != 0) {
+    if (loader) {
+      // Block i lands in slot i % SV, issued SV - 1 steps ahead. Before step
+      // i's barrier this wave waits for its loads of block i (the SV - 2
+      // younger blocks may stay in flight), so after the barrier the chain
+      // wave reads a whole block; the slot refilled after the barrier held
+      // block i - 1, which the chain wave finished reading before arriving.
+#pragma unroll
+      for (int u = 0; u < SV - 1; u++) ld.vload(u, arr(u) + wslot);
+      for (int64_t i0 = 0; i0 < nit0; i0 += SV) {
+#pragma unroll
+        for (int u = 0; u < SV; u++) {
+          __builtin_amdgcn_s_waitcnt(wait_vm((SV - 2) * (C::DK + C::DV)));
+          asm volatile("s_barrier" ::: "memory");
+          ld.vload(i0 + u + SV - 1, arr((u + SV - 1) % SV) + wslot);
+        }
+      }
+      // The merge below reuses the slots: no load may still be landing
+      // (those past the chain's blocks write zeros). Then the merge's barriers.
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        asm volatile("s_barrier" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+      }
+      return;
+    }
+  }
   // One block of this chain: keys in kr, values in value slot `slot`.
   constexpr int MKCT = MK ? CT : 1;
   auto compute = [&](const typename C::KRegs& kr, const unsigned short (&mk)[MKCT][8], int slot,
@@ -674,22 +711,34 @@ __global__ void __launch_bounds__(kThreads) sdpa_mfma_kernel(SdpaArgs p) {
   constexpr int U = lcm(PK + 1, SV);
   typename C::KRegs kr[PK + 1];
   typename C::MRegs mcur;  // MK == 2: this step's mask values
+  if constexpr (LW != 0) {
+    // Step i: after the barrier block i is in slot i % SV.
+    for (int64_t i0 = 0; i0 < nit0; i0 += U) {
 #pragma unroll
-  for (int u = 0; u < SV - 1; u++) ld.vload(u, arr(u) + wslot);
+      for (int u = 0; u < U; u++) {
+        const int64_t i = i0 + u;
+        asm volatile("s_barrier" ::: "memory");
+        if (i < nit) compute(kr[0], kr[0].m, u % SV, wave + kWaves * i);
+      }
+    }
+  } else {
 #pragma unroll
-  for (int u = 0; u < PK; u++) ld.kload(u, kr[u]);
-  for (int64_t i0 = 0; i0 < nit; i0 += U) {
+    for (int u = 0; u < SV - 1; u++) ld.vload(u, arr(u) + wslot);
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int64_t i = i0 + u;
-      if constexpr (MK == 2) ld.mload(i, mcur.m);
-      ld.kload(i + PK, kr[(u + PK) % (PK + 1)]);
-      ld.vload(i + SV - 1, arr((u + SV - 1) % SV) + wslot);
-      if (i < nit) {
-        if constexpr (MK == 2)
-          compute(kr[u % (PK + 1)], mcur.m, u % SV, wave + kWaves * i);
-        else
-          compute(kr[u % (PK + 1)], kr[u % (PK + 1)].m, u % SV, wave + kWaves * i);
+    for (int u = 0; u < PK; u++) ld.kload(u, kr[u]);
+    for (int64_t i0 = 0; i0 < nit; i0 += U) {
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int64_t i = i0 + u;
+        if constexpr (MK == 2) ld.mload(i, mcur.m);
+        ld.kload(i + PK, kr[(u + PK) % (PK + 1)]);
+        ld.vload(i + SV - 1, arr((u + SV - 1) % SV) + wslot);
+        if (i < nit) {
+          if constexpr (MK == 2)
+            compute(kr[u % (PK + 1)], mcur.m, u % SV, wave + kWaves * i);
+          else
+            compute(kr[u % (PK + 1)], kr[u % (PK + 1)].m, u % SV, wave + kWaves * i);
+        }
       }
     }
   }
@@ -1140,12 +1189,13 @@ constexpr SdpaKernelFn mfma_kernel() {
       return nullptr;
   } else if constexpr (SHAPE == SDPA_ROWS) {
     return sdpa_mfma_kernel<T, D, V, sdpa_rows_tiles(D, V), MASK ? 0 : PK, 2, WS, MASK ? 2 : 0,
-                            false>;
+                            false, 0>;
   } else if constexpr (SHAPE == SDPA_TILE) {
-    return sdpa_mfma_kernel<T, D, V, 1, PK, 2, WS, MK, false>;
+    return sdpa_mfma_kernel<T, D, V, 1, PK, 2, WS, MK, false, 0>;
   } else {
-    constexpr bool KLS = !MASK && D == 128 && V == 128;
-    return sdpa_mfma_kernel<T, D, V, 1, KLS ? 0 : PK, KLS ? 3 : 2, WS, MK, KLS>;
+    // Keys in LDS with loader waves (sdpa_loaders: the host launches 8 waves).
+    constexpr bool KLS = sdpa_loaders(D, V, SHAPE, MASK);
+    return sdpa_mfma_kernel<T, D, V, 1, KLS ? 0 : PK, KLS ? 3 : 2, WS, MK, KLS, KLS ? kWaves : 0>;
   }
 }
 
