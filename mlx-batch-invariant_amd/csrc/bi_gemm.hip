@@ -17,7 +17,7 @@ struct Geometry {
   int bm, bn, waves;
 };
 
-#define BI_GEO_ENTRY(id, bm, bn, wm, wn, nw, kb, ns) {bm, bn, nw},
+#define BI_GEO_ENTRY(id, bm, bn, wm, wn, nw, kb, ns, pl) {bm, bn, nw},
 constexpr Geometry kGeometries[] = {BI_GEOMETRIES(BI_GEO_ENTRY)};
 #undef BI_GEO_ENTRY
 constexpr int kNumGeometries = sizeof(kGeometries) / sizeof(kGeometries[0]);
@@ -47,8 +47,8 @@ int pick_geometry(int64_t M, int64_t N, int dtype) {
   if (M <= 64) return ceil_div(N, 32) >= 256 ? 5 : 1;
   // Small outputs (e.g. 256 x 512): 64 x 64 tiles would leave most CUs idle.
   if (ceil_div(M, 64) * ceil_div(N, 64) < 64) return 1;
-  // fp32 carries two accumulator chains: the 256 x 128 footprint would need
-  // more than the 256 registers a wave of an 8-wave workgroup can hold.
+  // fp32 carries two accumulator chains: the 256 x 128 footprint (12 waves,
+  // at most 168 registers each) is built for 16-bit types only.
   if (dtype != BI_F32 && ceil_div(M, 256) * ceil_div(N, 128) >= 200) return 4;
   if (ceil_div(M, 128) * ceil_div(N, 128) >= 160) return 3;
   return 2;

@@ -189,7 +189,10 @@ constexpr int waitcnt_vm_lgkm0(int vm) {
 
 // One workgroup computes a BM x BN tile of C over the whole of K.
 //   WM x WN compute waves own (BM / WM) x (BN / WN) sub-tiles; NW >= WM * WN
-//   waves in total, the extra waves only load.
+//   waves in total, the extra waves only load. PL: the loading waves issue
+//   every load and the compute waves none (a wave whose load issue stalls on
+//   a busy memory pipeline then holds up no matrix products); otherwise all
+//   NW waves share the loads.
 //   KB: bytes of each A / B row staged per pipeline stage (a multiple of 128).
 //   NS: stages in the LDS ring. Operands move global -> LDS with buffer loads
 //       that write LDS directly (no VGPR staging, no ds_write); NS - 1 stages
@@ -210,7 +213,8 @@ struct QSlot {
   unsigned short* z16;
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, int QB = 0>
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, int QB = 0,
+          bool PL = false>
 struct GemmTile {
   static constexpr int NT = 64 * NW;
   static constexpr int CW = WM * WN;                  // compute waves
@@ -226,13 +230,15 @@ struct GemmTile {
   static constexpr int LB = (B_CH + NT - 1) / NT;
   static constexpr int NN_CPR = BN * (int)sizeof(T) / 16;  // chunks per k-row, (K, N) B tile
   static constexpr int STAGE_CH = A_CH + B_CH;
-  static constexpr int DMA = STAGE_CH / 64 / NW;      // 1 KB LDS-DMA loads per wave per stage
+  static constexpr int LDW = PL ? NW - WM * WN : NW;  // waves that issue loads
+  static constexpr int DMA = STAGE_CH / 64 / LDW;     // 1 KB LDS-DMA loads per loading wave per stage
   static constexpr int CHAINS = sizeof(T) == 4 ? 2 : 1;    // fp32: chain per chunk-step parity
   static_assert(CW <= NW && FM >= 1 && FN >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "geometry");
   static_assert(KB % 128 == 0 && CS % 2 == 0, "stage bytes");
   static_assert(TB || (NN_CPR >= 1 && (NN_CPR & (NN_CPR - 1)) == 0), "bad (K,N) tile width");
-  static constexpr int DMA_A = A_CH / 64 / NW;      // of which A loads (the rest load B)
-  static_assert(A_CH % (64 * NW) == 0 && B_CH % (64 * NW) == 0, "stage must split into 1 KB loads");
+  static constexpr int DMA_A = A_CH / 64 / LDW;     // of which A loads (the rest load B)
+  static_assert(LDW >= 1, "PL needs loading waves");
+  static_assert(A_CH % (64 * LDW) == 0 && B_CH % (64 * LDW) == 0, "stage must split into 1 KB loads");
   static_assert(NS >= 2 && NS <= 8 && DMA * (NS - 2) <= 63, "ring depth");
 
   const T* __restrict__ A;
@@ -284,7 +290,8 @@ struct GemmTile {
   int32_t dma_kidx[DMA];
 
   __device__ __forceinline__ int dma_blk(int i) const {
-    return i < DMA_A ? i * NW + wave : (i - DMA_A) * NW + wave;
+    const int lw = PL ? wave - CW : wave;  // index among the loading waves
+    return i < DMA_A ? i * LDW + lw : (i - DMA_A) * LDW + lw;
   }
 
   __device__ __forceinline__ void init_dma() {
@@ -493,6 +500,34 @@ struct GemmTile {
   template <typename Slots>
   __device__ __forceinline__ void main_loop_dma(const Slots& slots, int64_t nst, bool computes,
                                                 f32x4_t (&acc)[CHAINS][FM][FN]) const {
+    if constexpr (PL) {
+      // The same rounds split by role: a loading wave waits for its own
+      // loads of stage s (those of s+1 .. s+NS-2 may stay in flight) before
+      // the barrier and refills the freed slot after it; a compute wave's
+      // LDS reads of the previous stage have returned before it arrives.
+      if (wave >= CW) {
+#pragma unroll
+        for (int u = 0; u < NS - 1; u++) dma(u, slots(u));
+        for (int64_t s0 = 0; s0 < nst; s0 += NS) {
+#pragma unroll
+          for (int u = 0; u < NS; u++) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DMA * (NS - 2)));
+            asm volatile("s_barrier" ::: "memory");
+            dma(s0 + u + NS - 1, slots((u + NS - 1) % NS));
+          }
+        }
+      } else {
+        for (int64_t s0 = 0; s0 < nst; s0 += NS) {
+#pragma unroll
+          for (int u = 0; u < NS; u++) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+            asm volatile("s_barrier" ::: "memory");
+            if (computes) compute_full(slots(u), acc);
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < NS - 1; u++) dma(u, slots(u));
     if (NW == CW || computes)
@@ -837,9 +872,9 @@ struct GemmTile {
   }
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB>
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, bool PL>
 __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
-  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB>;
+  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB, 0, PL>;
   constexpr int FM = Tile::FM, FN = Tile::FN, CHAINS = Tile::CHAINS;
   constexpr int AC = Tile::A_CH, BC = Tile::B_CH;
   // The LDS ring: NS stages, each an A and a B array (unused ones are a single chunk).
@@ -1050,23 +1085,27 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
 // Footprints of C per workgroup. Every entry runs the same per-element
 // arithmetic; the table only trades parallelism against operand reuse and
 // latency hiding. Columns: id, BM, BN, WM, WN, NW (waves), KB (stage bytes),
-// NS (LDS ring stages).
+// NS (LDS ring stages), PL (loading waves issue all loads).
 #define BI_GEOMETRIES(X)                  \
-  X(0, 16, 16, 1, 1, 4, 512, 4)           \
-  X(1, 64, 16, 4, 1, 4, 256, 4)           \
-  X(2, 64, 64, 2, 2, 8, 256, 4)           \
-  X(3, 128, 128, 4, 2, 8, 128, 4)         \
-  X(4, 256, 128, 4, 2, 8, 128, 3)         \
-  X(5, 64, 32, 4, 2, 8, 256, 3)
+  X(0, 16, 16, 1, 1, 4, 512, 4, 0)        \
+  X(1, 64, 16, 4, 1, 4, 256, 4, 0)        \
+  X(2, 64, 64, 2, 2, 8, 256, 4, 0)        \
+  X(3, 128, 128, 4, 2, 8, 128, 4, 0)      \
+  X(4, 256, 128, 4, 2, 12, 128, 3, 1)     \
+  X(5, 64, 32, 4, 2, 8, 256, 3, 0)
 
 using KernelFn = void (*)(GemmArgs);
 
 // Kernel for geometry g in the translation unit of element type T.
 template <typename T>
 KernelFn kernel_for(int g, bool trans_b) {
-#define BI_GEO_CASE(id, bm, bn, wm, wn, nw, kb, ns) \
-  case id: return trans_b ? gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true>  \
-                          : gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, false>;
+// fp32 carries two accumulator chains per element: with more than 8 waves
+// (at most 168 registers each) the 64 x 64 wave tiles do not fit.
+#define BI_GEO_CASE(id, bm, bn, wm, wn, nw, kb, ns, pl)                          \
+  case id:                                                                      \
+    if constexpr (sizeof(T) == 4 && nw > 8) return nullptr;                     \
+    else return trans_b ? gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, pl>  \
+                        : gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, false, pl>;
   switch (g) { BI_GEOMETRIES(BI_GEO_CASE) }
 #undef BI_GEO_CASE
   return nullptr;
@@ -1087,7 +1126,7 @@ KernelFn qkernel_gs(int group) {
 
 template <typename T>
 KernelFn qkernel_for(int g, int bits, int group) {
-#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns)                                \
+#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns, pl)                            \
   case id:                                                                          \
     if constexpr (bm * bn <= 128 * 128) {                                           \
       switch (bits) {                                                               \

@@ -44,7 +44,7 @@ def test_abi_version_and_geometry_table():
     geos = bi.geometries()
     assert len(geos) == L.bi_gemm_num_geometries() >= 2
     for bm, bn, w in geos:
-        assert bm % 16 == 0 and bn % 16 == 0 and w in (1, 2, 4, 8, 16)
+        assert bm % 16 == 0 and bn % 16 == 0 and 1 <= w <= 16  # a workgroup holds at most 16 waves
     assert L.bi_gemm_geometry_info(len(geos), None, None, None) == _lib.EINVAL
     for M in (1, 16, 17, 64, 65, 256, 4096):
         assert 0 <= L.bi_gemm_pick_geometry(M, 4096, 4096, _lib.BF16, 1) < len(geos)
@@ -66,7 +66,7 @@ def test_footprint_policy():
     assert pick(256, 512) == (64, 16, 4)                        # small output
     assert pick(256, 4096) == (64, 64, 8)
     assert pick(256, 11008) == (128, 128, 8)
-    assert pick(256, 32000) == (256, 128, 8)                    # the bench's dominant shape
+    assert pick(256, 32000) == (256, 128, 12)                   # the bench's dominant shape
     assert pick(256, 32000, _lib.F32) == (128, 128, 8)          # fp32: registers
 
 
