@@ -1112,8 +1112,9 @@ KernelFn kernel_for(int g, bool trans_b) {
 }
 
 // Quantized-B kernel for geometry g (16-bit element types; (N, K) packed B).
-// The 256 x 128 footprint is not built: with the loads in flight in
-// registers it would spill.
+// Footprints above 128 x 128 and those whose loading waves issue every load
+// (PL) are not built: the quantized kernel's loads land in registers of the
+// computing waves, and larger tiles would spill them.
 template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int QB>
 KernelFn qkernel_gs(int group) {
   switch (group) {
@@ -1128,7 +1129,7 @@ template <typename T>
 KernelFn qkernel_for(int g, int bits, int group) {
 #define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns, pl)                            \
   case id:                                                                          \
-    if constexpr (bm * bn <= 128 * 128) {                                           \
+    if constexpr (bm * bn <= 128 * 128 && !pl) {                                    \
       switch (bits) {                                                               \
         case 2: return qkernel_gs<T, bm, bn, wm, wn, nw, kb, 2>(group);             \
         case 4: return qkernel_gs<T, bm, bn, wm, wn, nw, kb, 4>(group);             \
