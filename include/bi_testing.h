@@ -27,10 +27,14 @@ int bi_gemm_num_geometries(void);
  * workgroup. Returns BI_EINVAL for an unknown g. */
 int bi_gemm_geometry_info(int g, int* block_m, int* block_n, int* waves);
 
-/* The geometry bi_gemm would launch for this problem. */
+/* The geometry bi_gemm would launch for this problem with 16-byte aligned
+ * operands (for others it replaces a footprint that takes aligned operands
+ * only, the 256 x 128 one, by 128 x 128). */
 int bi_gemm_pick_geometry(int64_t M, int64_t N, int64_t K, int dtype, int trans_b);
 
-/* bi_gemm with the geometry forced to `g` (same arguments and semantics). */
+/* bi_gemm with the geometry forced to `g` (same arguments and semantics);
+ * BI_EUNSUPPORTED where g is not built for the dtype or takes aligned
+ * operands only and these are not. */
 int bi_gemm_with_geometry(const void* a, const void* b, const void* bias, void* out,
                           int64_t M, int64_t N, int64_t K, int dtype, int trans_b,
                           float alpha, float beta, int g, void* hip_stream);

@@ -15,9 +15,10 @@ using bi_gemm_dev::KernelFn;
 
 struct Geometry {
   int bm, bn, waves;
+  bool pl;  // loading waves issue every load; 16-byte aligned operands only
 };
 
-#define BI_GEO_ENTRY(id, bm, bn, wm, wn, nw, kb, ns, pl) {bm, bn, nw},
+#define BI_GEO_ENTRY(id, bm, bn, wm, wn, nw, kb, ns, pl) {bm, bn, nw, pl != 0},
 constexpr Geometry kGeometries[] = {BI_GEOMETRIES(BI_GEO_ENTRY)};
 #undef BI_GEO_ENTRY
 constexpr int kNumGeometries = sizeof(kGeometries) / sizeof(kGeometries[0]);
@@ -91,6 +92,17 @@ VecFlags vec_flags(const void* a, const void* b, int64_t N, int64_t K, int dtype
   return v;
 }
 
+// The geometry bi_gemm launches: pick_geometry's, unless that one takes
+// aligned operands only and these are not; then the 128 x 128 footprint.
+int pick_for(const void* a, const void* b, int64_t M, int64_t N, int64_t K, int dtype, int trans_b) {
+  int g = pick_geometry(M, N, dtype);
+  if (kGeometries[g].pl) {
+    const VecFlags v = vec_flags(a, b, N, K, dtype, trans_b, kGeometries[g]);
+    if (!(v.a && v.b)) g = 3;
+  }
+  return g;
+}
+
 // start/stop (optional): hipEvents that receive the dispatch's own start and
 // end timestamps (hipExtLaunchKernelGGL), so timing a launch adds no marker
 // packets around it.
@@ -111,6 +123,8 @@ int launch(const void* a, const void* b, const void* bias, void* out, int64_t M,
   p.alpha = alpha;
   p.beta = beta;
   const VecFlags v = vec_flags(a, b, N, K, dtype, trans_b, G);
+  if (G.pl && !(v.a && v.b))
+    return bi::fail(BI_EUNSUPPORTED, "bi_gemm: geometry %d takes 16-byte aligned operands only", g);
   p.vec_a = v.a;
   p.vec_b = v.b;
   const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n;
@@ -136,8 +150,8 @@ extern "C" int bi_gemm(const void* a, const void* b, const void* bias, void* out
                        void* hip_stream) {
   const int rc = validate(a, b, out, M, N, K, dtype, trans_b);
   if (rc != BI_OK || M == 0 || N == 0) return rc;
-  return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta, pick_geometry(M, N, dtype),
-                hip_stream);
+  return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta,
+                pick_for(a, b, M, N, K, dtype, trans_b), hip_stream);
 }
 
 extern "C" int bi_gemm_timed(const void* a, const void* b, const void* bias, void* out,
@@ -145,8 +159,8 @@ extern "C" int bi_gemm_timed(const void* a, const void* b, const void* bias, voi
                              float beta, void* start_event, void* stop_event, void* hip_stream) {
   const int rc = validate(a, b, out, M, N, K, dtype, trans_b);
   if (rc != BI_OK || M == 0 || N == 0) return rc;
-  return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta, pick_geometry(M, N, dtype),
-                hip_stream, start_event, stop_event);
+  return launch(a, b, bias, out, M, N, K, dtype, trans_b, alpha, beta,
+                pick_for(a, b, M, N, K, dtype, trans_b), hip_stream, start_event, stop_event);
 }
 
 extern "C" int bi_gemm_num_geometries(void) { return kNumGeometries; }

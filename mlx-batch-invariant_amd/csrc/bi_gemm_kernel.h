@@ -933,9 +933,13 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
   t.init_lds_offsets();
   if (p.vec_a && p.vec_b) {
     t.init_buffers();
-    t.init_dma();
+    // With PL only the loading waves need the load addressing.
+    if (!PL || t.wave >= Tile::CW) t.init_dma();
     t.main_loop_dma(slots, nst, computes, acc);
-  } else {
+  } else if constexpr (!PL) {
+    // PL footprints take 16-byte aligned operands only: the host launches
+    // another footprint for the others (the slow path's registers would make
+    // the whole kernel spill).
     t.main_loop_slow(slots, nst, nsteps, computes, acc);
   }
 

@@ -134,6 +134,40 @@ def test_all_geometries_agree(cuda, trans_b):
     assert {gi for gi, dn in ran if dn != "float32"} == set(range(len(geos)))
 
 
+def test_unaligned_operands_leave_the_aligned_only_footprint(cuda):
+    """The 256x128 footprint (its loading waves issue every load) takes
+    16-byte aligned operands only: forcing it on others raises, and bi_gemm
+    launches the 128x128 footprint instead. Misaligned bases and a K that is
+    not a multiple of 8 give the bits of the same values in aligned storage
+    and of every footprint that takes them."""
+    from mlx_batch_invariant import _lib
+    geos = _gemm.geometries()
+    g_pl = geos.index((256, 128, 12))
+    L = _lib.lib()
+    for dname, dtype in DTYPES[1:]:
+        for K in (1024, 1001):
+            M, N = 256, 25600
+            assert L.bi_gemm_pick_geometry(M, N, K, _lib.DTYPE_CODES[dtype], 0) == g_pl
+            a = rn((M, K), dtype, 31, device=cuda)
+            b = rn((K, N), dtype, 32, std=K ** -0.5, device=cuda)
+            ref = bits(bi.matmul(a, b))
+            buf = torch.empty(M * K + 1, dtype=dtype, device=cuda)
+            au = buf[1:].view(M, K)
+            au.copy_(a)
+            assert au.data_ptr() % 16 != 0
+            assert (bits(bi.matmul(au, b)) == ref).all(), "%s K=%d: misaligned A" % (dname, K)
+            with pytest.raises(NotImplementedError):
+                _gemm._gemm(au, b, None, False, geometry=g_pl)
+            if K % 8:
+                with pytest.raises(NotImplementedError):
+                    _gemm._gemm(a, b, None, False, geometry=g_pl)
+            else:
+                assert (bits(_gemm._gemm(a, b, None, False, geometry=g_pl)) == ref).all()
+            for gi in (2, 3):
+                assert (bits(_gemm._gemm(au, b, None, False, geometry=gi)) == ref).all(), (
+                    "%s K=%d geometry %s" % (dname, K, geos[gi]))
+
+
 def test_kn_and_nk_layouts_agree(cuda):
     """matmul on a (K, N) weight and linear on the same weight stored (N, K)
     feed the MFMAs identically, so they give the same bits; a transposed view
