@@ -113,6 +113,21 @@ __device__ inline int xcd_remap(int w, int total) {
   return w;
 }
 
+// Logical tile -> (row block, column block): groups of 4 row blocks, row
+// blocks fastest within a group, then column blocks. The tiles an XCD runs
+// at once then span about 4 row blocks of A and a few column blocks of B,
+// which its L2 serves to each other (a tall column of row blocks would
+// stream all of A through it). With 4 or fewer row blocks this is plain
+// column-major order.
+__device__ inline void tile_coords(int tile, int tiles_m, int tiles_n, int& mi, int& ni) {
+  constexpr int kGroupM = 4;
+  const int gsz = kGroupM * tiles_n;
+  const int grp = tile / gsz, within = tile % gsz;
+  const int rows = tiles_m - grp * kGroupM < kGroupM ? tiles_m - grp * kGroupM : kGroupM;
+  mi = grp * kGroupM + within % rows;
+  ni = within / rows;
+}
+
 // 16-byte chunk of row `row` of a row-major matrix with leading dimension
 // `ld`, starting at element k, read element by element; elements of rows at
 // or past `rows` or at or past column `limit` are zero. The path for operands
@@ -911,8 +926,10 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
   t.g = t.lane >> 4;
   t.r16 = t.lane & 15;
   const int tile = xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n);
-  t.m0 = (int64_t)(tile % p.tiles_m) * BM;
-  t.n0 = (int64_t)(tile / p.tiles_m) * BN;
+  int mi, ni;
+  tile_coords(tile, p.tiles_m, p.tiles_n, mi, ni);
+  t.m0 = (int64_t)mi * BM;
+  t.n0 = (int64_t)ni * BN;
 
   const int64_t M = t.M, N = t.N, K = t.K;
   const int64_t nst = (K + Tile::EPS - 1) / Tile::EPS;
@@ -1047,8 +1064,10 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
   t.g = t.lane >> 4;
   t.r16 = t.lane & 15;
   const int tile = xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n);
-  t.m0 = (int64_t)(tile % p.tiles_m) * BM;
-  t.n0 = (int64_t)(tile / p.tiles_m) * BN;
+  int mi, ni;
+  tile_coords(tile, p.tiles_m, p.tiles_n, mi, ni);
+  t.m0 = (int64_t)mi * BM;
+  t.n0 = (int64_t)ni * BN;
 
   const int64_t M = t.M, N = t.N, K = t.K;
   const int64_t nst = (K + Tile::EPS - 1) / Tile::EPS;
