@@ -566,15 +566,20 @@ struct GemmTile {
   // roundings only -- the reference's fp32 product with its fp32 weights to
   // within fp32 accumulation error -- and a fixed sequence per output element.
   static constexpr int QP = NW == 8 ? 2 : 4;  // stages of loads in flight (registers)
+  // Threads that load and stage the quantized operands: the waves that do
+  // not compute, when there are such (the computing waves then only read LDS
+  // and run the MFMAs and folds), else all.
+  static constexpr int QNT = (QB != 0 && NW > CW) ? 64 * (NW - CW) : NT;
+  static constexpr int QLA = (A_CH + QNT - 1) / QNT;
   static constexpr int GPS = EPS / 32;        // most groups that end in one stage
   static constexpr int QSB = BN * GPS;        // scale/bias entries staged per stage
-  static constexpr int LSB = (QSB + NT - 1) / NT;
+  static constexpr int LSB = (QSB + QNT - 1) / QNT;
   // B is loaded in units of CPT consecutive chunks of a row: one aligned
   // dword (2 and 4 bits) or dword pair (8 bits) per unit.
   static constexpr int CPT = QB == 2 ? 2 : 1;  // (1 for the dense kernels, QB = 0)
   static constexpr int RCU = RC / CPT;        // units per tile row per stage
   static constexpr int B_U = BN * RCU;        // units per stage
-  static constexpr int LBU = (B_U + NT - 1) / NT;
+  static constexpr int LBU = (B_U + QNT - 1) / QNT;
   static_assert(QB == 0 || (TB && sizeof(T) == 2 && (QB == 2 || QB == 4 || QB == 8)),
                 "quantized B: (N, K) layout, 16-bit elements, 2/4/8 bits");
   static_assert(RC % CPT == 0, "stage holds whole units");
@@ -583,7 +588,7 @@ struct GemmTile {
   // wave wait for every load in flight, the prefetched stages with them.
   using QWord = typename std::conditional<QB == 8, uint2, uint32_t>::type;
   struct QStage {
-    uint4 a[LA];
+    uint4 a[QLA];
     QWord w[LBU];                     // packed codes of unit i
     unsigned short sc[LSB], zb[LSB];  // scale and bias of entry i, element bits
   };
@@ -595,8 +600,9 @@ struct GemmTile {
   // the K index (or group within the stage) that decides whether a load is
   // inside the operand. Stage s adds s * EPS elements (s * EPS * QB / 8 bytes
   // of B, glo(s) groups).
-  uint32_t qa_off[LA], qb_off[LBU], qs_off[LSB];
-  int32_t qa_k[LA], qb_k[LBU], qs_gi[LSB];
+  uint32_t qa_off[QLA], qb_off[LBU], qs_off[LSB];
+  int32_t qa_k[QLA], qb_k[LBU], qs_gi[LSB];
+  int qtid;  // index among the QNT loading threads
 
   __device__ __forceinline__ void init_buffers_q(const GemmArgs& p) {
     constexpr int64_t E = sizeof(T);
@@ -609,22 +615,22 @@ struct GemmTile {
     rs_src = make_rsrc(static_cast<const T*>(p.qs) + n0 * G, rows * G * E);
     rz_src = make_rsrc(static_cast<const T*>(p.qz) + n0 * G, rows * G * E);
 #pragma unroll
-    for (int i = 0; i < LA; i++) {
-      const int q = tid + i * NT, r = q / RC, c = q % RC;
+    for (int i = 0; i < QLA; i++) {
+      const int q = qtid + i * QNT, r = q / RC, c = q % RC;
       qa_off[i] = (uint32_t)((r * K + c * EPC) * E);
-      qa_k[i] = (A_CH % NT == 0 || q < A_CH) ? c * EPC : INT32_MAX;
+      qa_k[i] = (A_CH % QNT == 0 || q < A_CH) ? c * EPC : INT32_MAX;
     }
 #pragma unroll
     for (int i = 0; i < LBU; i++) {
-      const int q = tid + i * NT, r = q / RCU, c = (q % RCU) * CPT;
+      const int q = qtid + i * QNT, r = q / RCU, c = (q % RCU) * CPT;
       qb_off[i] = (uint32_t)(r * qrow_bytes + c * EPC * QB / 8);
-      qb_k[i] = (B_U % NT == 0 || q < B_U) ? c * EPC : INT32_MAX;
+      qb_k[i] = (B_U % QNT == 0 || q < B_U) ? c * EPC : INT32_MAX;
     }
 #pragma unroll
     for (int i = 0; i < LSB; i++) {
-      const int e = tid + i * NT, r = e / GPS, gi = e % GPS;
+      const int e = qtid + i * QNT, r = e / GPS, gi = e % GPS;
       qs_off[i] = (uint32_t)((r * G + gi) * E);
-      qs_gi[i] = (QSB % NT == 0 || e < QSB) ? gi : INT32_MAX;
+      qs_gi[i] = (QSB % QNT == 0 || e < QSB) ? gi : INT32_MAX;
     }
   }
 
@@ -638,7 +644,7 @@ struct GemmTile {
     const uint32_t a_step = (uint32_t)(s * EPS) * E;
     const uint32_t b_step = (uint32_t)(s * EPS) * QB / 8;
 #pragma unroll
-    for (int i = 0; i < LA; i++)
+    for (int i = 0; i < QLA; i++)
       st.a[i] = buffer_chunk(ra_src, qa_k[i] < kleft ? qa_off[i] + a_step : kOutOfRange);
 #pragma unroll
     for (int i = 0; i < LBU; i++) {
@@ -697,17 +703,17 @@ struct GemmTile {
   // dense (N, K) tile layout, and the stage's scale/bias entries.
   __device__ __forceinline__ void qstore(QSlot sl, const QStage& st) const {
 #pragma unroll
-    for (int i = 0; i < LA; i++) {
-      const int q = tid + i * NT;
-      if (A_CH % NT == 0 || q < A_CH) {
+    for (int i = 0; i < QLA; i++) {
+      const int q = qtid + i * QNT;
+      if (A_CH % QNT == 0 || q < A_CH) {
         const int r = q / RC, c = q % RC;
         sl.a[r * RC + (c ^ swz_k<RC>(r))] = st.a[i];
       }
     }
 #pragma unroll
     for (int i = 0; i < LBU; i++) {
-      const int q = tid + i * NT;
-      if (B_U % NT == 0 || q < B_U) {
+      const int q = qtid + i * QNT;
+      if (B_U % QNT == 0 || q < B_U) {
         const int r = q / RCU, c = (q % RCU) * CPT;
         uint32_t d[ND];
         spread_codes(st.w[i], d);
@@ -724,8 +730,8 @@ struct GemmTile {
     }
 #pragma unroll
     for (int i = 0; i < LSB; i++) {
-      const int e = tid + i * NT;
-      if (QSB % NT == 0 || e < QSB) {
+      const int e = qtid + i * QNT;
+      if (QSB % QNT == 0 || e < QSB) {
         sl.s16[e] = st.sc[i];
         sl.z16[e] = st.zb[i];
       }
@@ -831,7 +837,7 @@ struct GemmTile {
   // stages, so ring indices are compile-time). Before a slot is rewritten,
   // the barrier guarantees every wave finished reading it (LDS reads retire
   // before the barrier: lgkmcnt(0)).
-  template <bool COMPUTE, int GS, typename QSlots>
+  template <bool COMPUTE, bool LOAD, int GS, typename QSlots>
   __device__ __forceinline__ void q_rounds(const QSlots& slots, int64_t nst, int64_t nsteps,
                                            QStage (&q)[QP], f32x4_t (&acc)[FM][FN],
                                            f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
@@ -840,8 +846,10 @@ struct GemmTile {
       for (int u = 0; u < QP; u++) {
         __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
         asm volatile("s_barrier" ::: "memory");
-        qstore(slots((u + 1) & 1), q[(u + 1) % QP]);
-        qload(s0 + u + 1 + QP, q[(u + 1) % QP]);
+        if constexpr (LOAD) {
+          qstore(slots((u + 1) & 1), q[(u + 1) % QP]);
+          qload(s0 + u + 1 + QP, q[(u + 1) % QP]);
+        }
         if constexpr (COMPUTE)
           q_compute<GS>(slots(u & 1), s0 + u, steps_of(nsteps, s0 + u), acc, P, X);
       }
@@ -860,14 +868,29 @@ struct GemmTile {
       for (int jn = 0; jn < FN; jn++) P[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
     QStage q[QP];
+    if constexpr (QNT < NT) {
+      // Loading waves stage every operand; computing waves only compute.
+      if (wave >= CW) {
+#pragma unroll
+        for (int u = 0; u < QP; u++) qload(u, q[u]);
+        qstore(slots(0), q[0]);
+        qload(QP, q[0]);
+        q_rounds<false, true, GS>(slots, nst, nsteps, q, acc, P, X);
+      } else if (computes) {
+        q_rounds<true, false, GS>(slots, nst, nsteps, q, acc, P, X);
+      } else {
+        q_rounds<false, false, GS>(slots, nst, nsteps, q, acc, P, X);
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < QP; u++) qload(u, q[u]);
     qstore(slots(0), q[0]);
     qload(QP, q[0]);
     if (computes)
-      q_rounds<true, GS>(slots, nst, nsteps, q, acc, P, X);
+      q_rounds<true, true, GS>(slots, nst, nsteps, q, acc, P, X);
     else
-      q_rounds<false, GS>(slots, nst, nsteps, q, acc, P, X);
+      q_rounds<false, true, GS>(slots, nst, nsteps, q, acc, P, X);
   }
 
   // Register-staged path (unaligned operands): two slots, double buffered.
@@ -1057,6 +1080,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
   t.N = p.N;
   t.K = p.K;
   t.tid = threadIdx.x;
+  t.qtid = t.tid - (Tile::NT - Tile::QNT);
   t.lane = t.tid & 63;
   t.wave = __builtin_amdgcn_readfirstlane(t.tid >> 6);
   t.wm = (t.wave % Tile::CW) / WN;
