@@ -115,6 +115,33 @@ def test_every_shape_gives_the_same_bits(cuda, D, V):
                         dname, D, V, label, s, d)
 
 
+def test_short_contexts_through_the_loader_wave_shapes(cuda):
+    """Decode at D = V = 128 without an array mask takes the dim-split shapes
+    with loader waves, whose chains can hold no block at all (N < 97) or
+    different block counts. Contexts of 1 to 129 keys, causal and not, with
+    and without sinks: the picked shape gives the bits of the rows and
+    one-tile shapes, and a single key returns its value row exactly."""
+    H, Hkv, D = 32, 8, 128
+    for dname, dtype in LOW:
+        for B in (1, 8):
+            for N in (1, 5, 32, 33, 97, 100, 129):
+                q = rn((B, H, 1, D), dtype, 301 + N, device=cuda)
+                k = rn((B, Hkv, N, D), dtype, 302 + N, device=cuda)
+                v = rn((B, Hkv, N, D), dtype, 303 + N, device=cuda)
+                sinks = rn((H,), dtype, 304, device=cuda)
+                shape = _attention.launch_shape(q, k, v)
+                assert shape in (_lib.SDPA_SPLIT2, _lib.SDPA_SPLIT4, _lib.SDPA_SPLIT8), (B, N, shape)
+                for spec, sk in ((None, None), ("end", None), (None, sinks)):
+                    y = run(q, k, v, spec, sinks=sk)
+                    case = "%s B=%d N=%d %s sinks=%s shape %d" % (dname, B, N, spec, sk is not None, shape)
+                    for forced in (_lib.SDPA_TILE, _lib.SDPA_ROWS):
+                        d = int((bits(run(q, k, v, spec, shape=forced, sinks=sk)) != bits(y)).sum())
+                        assert d == 0, "%s: forced %d: %d differ" % (case, forced, d)
+                    if N == 1 and sk is None:
+                        want = v.repeat_interleave(H // Hkv, dim=1)
+                        assert np.array_equal(bits(y), bits(want.contiguous())), case
+
+
 def _oracle_rows(q, k, v, spec, rows, b, dname):
     """float64 and reference-order fp32 results for query rows `rows` of batch
     entry b (every head), each row as a one-row problem."""
