@@ -1019,19 +1019,29 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
     constexpr int SOFF = (slot - h * GP) * C::SLOT * 16;
     // Scores: S^T tiles (16 keys x 16 columns); lane (g, r16) holds keys
     // 16kt + 4g + e of column r16.
+    // Both key halves' reads are issued first; the first half's products run
+    // while the second half's reads are in flight.
     f32x4_t sc[2];
+    {
+      u32x4_t kl[2][NQ];
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-      u32x4_t kl[NQ];
+      for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int i = 0; i < NQ; i++) kl[i] = ds_read_b128_at(kofs[h][i], SOFF + kt * 16 * CH * 16);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (int i = 0; i < NQ; i++) kl[kt][i] = ds_read_b128_at(kofs[h][i], SOFF + kt * 16 * CH * 16);
+      asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(NQ) : "memory");
 #pragma unroll
-      for (int i = 0; i < NQ; i++) asm volatile("" : "+v"(kl[i]));
-      sc[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < NQ; i++) asm volatile("" : "+v"(kl[0][i]));
+      sc[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < NQ; i++)
-        sc[kt] = mma32(T(0), __builtin_bit_cast(uint4, kl[i]), qt[i], sc[kt]);
+        sc[0] = mma32(T(0), __builtin_bit_cast(uint4, kl[0][i]), qt[i], sc[0]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < NQ; i++) asm volatile("" : "+v"(kl[1][i]));
+      sc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < NQ; i++)
+        sc[1] = mma32(T(0), __builtin_bit_cast(uint4, kl[1][i]), qt[i], sc[1]);
     }
     // V^T blocks (dims 16db .., keys 16kt + 4g ..): lane r16 receives
     // V[16kt + 4g + t][16db + r16]. Read before the softmax, which hides
