@@ -404,7 +404,7 @@ struct Chain {
 // no load issue (which stalls while the memory pipeline is busy).
 template <typename T, int D, int V, int CT, int PK, int SV, int WS, int MK, bool KL, int LW>
 __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs p) {
-  static_assert(LW == 0 || (LW == kWaves && KL && PK == 0), "loader waves: one per chain");
+  static_assert(LW == 0 || (LW == kWaves && KL && PK == 0 && SV >= 3), "loader waves: one per chain");
   using C = Chain<T, D, V, CT, PK, SV, WS, MK, KL>;
   constexpr int NQ = C::NQ, NB = C::NB, VCH = C::VCH;
   constexpr int COLS = 16 * CT;  // columns per workgroup
@@ -486,24 +486,33 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
   const int wslot = wave * C::VSLOT;  // this wave's slot within each array
   C ld;
   ld.init(p, b, kvh, ws, wave, nit, lane, mrow, kmax);
-  // With loader waves every wave runs chain 0's number of steps (the most),
-  // one barrier per step.
+  // With loader waves every wave runs the same number of steps (chain 0 has
+  // the most blocks), one barrier each. PIPE (four slots or more): at step j
+  // a chain wave reads and scores the keys of block j while it finishes block
+  // j - 1, so there are nit0 + 1 steps and blocks are issued SV - 2 steps
+  // ahead; otherwise step j computes block j, issued SV - 1 steps ahead
+  // (two steps at the slot counts built, three and four).
   const int64_t nit0 = nblk > 0 ? (nblk + kWaves - 1) / kWaves : 0;
+  constexpr bool PIPE = LW != 0 && SV >= 4;
+  constexpr int AHEAD = PIPE ? SV - 2 : SV - 1;
+  const int64_t steps = PIPE ? nit0 + 1 : nit0;
   if constexpr (LW != 0) {
     if (loader) {
-      // Block i lands in slot i % SV, issued SV - 1 steps ahead. Before step
-      // i's barrier this wave waits for its loads of block i (the SV - 2
-      // younger blocks may stay in flight), so after the barrier the chain
-      // wave reads a whole block; the slot refilled after the barrier held
-      // block i - 1, which the chain wave finished reading before arriving.
+      // Block j lands in slot j % SV. Before barrier j this wave waits for
+      // its loads of block j (the AHEAD - 1 younger blocks may stay in
+      // flight), so after the barrier the chain wave reads whole blocks. The
+      // slot refilled after barrier j held block j + AHEAD - SV, which the
+      // chain wave finished reading before it arrived (PIPE: block j - 2,
+      // whose values were read at step j - 1; else block j - 1).
 #pragma unroll
-      for (int u = 0; u < SV - 1; u++) ld.vload(u, arr(u) + wslot);
-      for (int64_t i0 = 0; i0 < nit0; i0 += SV) {
+      for (int u = 0; u < AHEAD; u++) ld.vload(u, arr(u) + wslot);
+      for (int64_t j0 = 0; j0 < steps; j0 += SV) {
 #pragma unroll
         for (int u = 0; u < SV; u++) {
-          __builtin_amdgcn_s_waitcnt(wait_vm((SV - 2) * (C::DK + C::DV)));
+          if (j0 + u >= steps) break;
+          __builtin_amdgcn_s_waitcnt(wait_vm((AHEAD - 1) * (C::DK + C::DV)));
           asm volatile("s_barrier" ::: "memory");
-          ld.vload(i0 + u + SV - 1, arr((u + SV - 1) % SV) + wslot);
+          ld.vload(j0 + u + AHEAD, arr((u + AHEAD) % SV) + wslot);
         }
       }
       // The merge below reuses the slots: no load may still be landing
@@ -517,16 +526,11 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
       return;
     }
   }
-  // One block of this chain: keys in kr, values in value slot `slot`.
-  constexpr int MKCT = MK ? CT : 1;
-  auto compute = [&](const typename C::KRegs& kr, const unsigned short (&mk)[MKCT][8], int slot,
-                     int64_t blk) __attribute__((always_inline)) {
-    // Keys from the slot (KL): the slot's loads have landed (at most VWAIT
-    // younger operations in flight), then lane (r16, g) reads chunk 4q + g of
-    // key 16kt + r16.
-    u32x4_t kl[KL ? 2 : 1][KL ? NQ : 1];
+  // Keys of slot `slot` (KL) into kl: lane (r16, g) reads chunk 4q + g of
+  // key 16kt + r16. Issued only; the caller waits (lgkmcnt) before use.
+  using KL_t = u32x4_t[KL ? 2 : 1][KL ? NQ : 1];
+  auto kread = [&](int slot, KL_t& kl) __attribute__((always_inline)) {
     if constexpr (KL) {
-      __builtin_amdgcn_s_waitcnt(wait_vm(C::VWAIT));
       const uint32_t ks = (uint32_t)(uintptr_t)(lds_void_t*)(arr(slot) + wslot);
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
@@ -535,15 +539,19 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
           const int r = 16 * kt + r16;
           kl[kt][i] = ds_read_b128(ks + (r * C::CH + ((4 * i + g) ^ C::swz_k(r))) * 16);
         }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+  };
+  // Scores: S^T tiles (16 keys x 16 columns); lane (g, r16) holds keys
+  // 16kt + 4g + e of column r16. Keys from kr, or (KL) from kl once its reads
+  // have returned.
+  auto scores = [&](const typename C::KRegs& kr, KL_t& kl, f32x4_t (&sc)[CT][2])
+                    __attribute__((always_inline)) {
+    if constexpr (KL) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
 #pragma unroll
         for (int i = 0; i < NQ; i++) asm volatile("" : "+v"(kl[kt][i]));
     }
-    // Scores: S^T tiles (16 keys x 16 columns); lane (g, r16) holds keys
-    // 16kt + 4g + e of column r16.
-    f32x4_t sc[CT][2];
 #pragma unroll
     for (int ct = 0; ct < CT; ct++)
 #pragma unroll
@@ -555,6 +563,12 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
           sc[ct][kt] = mma32(T(0), a, qt[ct][i], sc[ct][kt]);
         }
       }
+  };
+  // Block blk of this chain given its scores: online softmax, rescale, and
+  // o += P . V with the values in value slot `slot`.
+  constexpr int MKCT = MK ? CT : 1;
+  auto update = [&](const f32x4_t (&sc)[CT][2], const unsigned short (&mk)[MKCT][8], int slot,
+                    int64_t blk) __attribute__((always_inline)) {
     // Key indices fit in 32 bits (the host checks N < 2^31).
     const int key0 = (int)blk * kBlk + 4 * g;
     uint2 ph[CT][2], pl[CT][2];
@@ -703,6 +717,20 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
       }
     }
   };
+  // One block of this chain: keys in kr (or, KL, in slot `slot` beside the
+  // values, landed with at most VWAIT younger operations in flight).
+  auto compute = [&](const typename C::KRegs& kr, const unsigned short (&mk)[MKCT][8], int slot,
+                     int64_t blk) __attribute__((always_inline)) {
+    KL_t kl;
+    if constexpr (KL) {
+      __builtin_amdgcn_s_waitcnt(wait_vm(C::VWAIT));
+      kread(slot, kl);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    f32x4_t sc[CT][2];
+    scores(kr, kl, sc);
+    update(sc, mk, slot, blk);
+  };
 
   // Block i of the chain: keys loaded at step i - PK, values at step
   // i - SV + 1 into slot i % SV. The loop is unrolled over U steps (the
@@ -711,14 +739,37 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
   constexpr int U = lcm(PK + 1, SV);
   typename C::KRegs kr[PK + 1];
   typename C::MRegs mcur;  // MK == 2: this step's mask values
-  if constexpr (LW != 0) {
-    // Step i: after the barrier block i is in slot i % SV.
-    for (int64_t i0 = 0; i0 < nit0; i0 += U) {
+  if constexpr (PIPE) {
+    // Step j: after the barrier blocks up to j are in their slots. The keys
+    // of block j are read and scored while block j - 1 (whose scores the
+    // previous step left in sp) finishes: the two are independent, so each
+    // hides the other's latency. Every product is the one compute() makes.
+    f32x4_t sp[CT][2];
+    for (int64_t j0 = 0; j0 < steps; j0 += SV) {
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int64_t i = i0 + u;
+      for (int u = 0; u < SV; u++) {
+        const int64_t j = j0 + u;
+        if (j >= steps) break;
         asm volatile("s_barrier" ::: "memory");
-        if (i < nit) compute(kr[0], kr[0].m, u % SV, wave + kWaves * i);
+        // From step nit on, the slot's stale keys are read and scored too
+        // (unconditionally, so no copies of the registers): those scores
+        // are never used.
+        KL_t kl;
+        kread(u, kl);
+        if (j >= 1 && j <= nit) update(sp, kr[0].m, (u + SV - 1) % SV, wave + kWaves * (j - 1));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        scores(kr[0], kl, sp);
+      }
+    }
+  } else if constexpr (LW != 0) {
+    // Step j: after the barrier block j is in slot j % SV.
+    for (int64_t j0 = 0; j0 < steps; j0 += SV) {
+#pragma unroll
+      for (int u = 0; u < SV; u++) {
+        const int64_t j = j0 + u;
+        if (j >= steps) break;
+        asm volatile("s_barrier" ::: "memory");
+        if (j < nit) compute(kr[0], kr[0].m, u, wave + kWaves * j);
       }
     }
   } else {
@@ -1180,11 +1231,17 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
   }
 }
 
+// Slots of a loader-wave shape: four (a block lands two steps before its
+// keys are read) where they fit the 160 KB of LDS, else three (one step).
+constexpr int sdpa_loader_slots(int D, int V, int WS) {
+  return 4 * kWaves * (kBlk * D / 8 + kBlk * (V / WS) / 8) * 16 <= 160 * 1024 ? 4 : 3;
+}
+
 // Kernel of launch shape `SHAPE` (SdpaShape) for head dims (D, V). The rows
 // shape with an array mask loads the mask values at the start of their own
 // block and no keys ahead, which keeps two workgroups per CU within the
 // registers; the split shapes without a mask at D = V = 128 load the keys
-// through LDS by contiguous loads (three slots). Wide heads (D or V above
+// through LDS by contiguous loads (sdpa_loader_slots). Wide heads (D or V above
 // 128) load no keys ahead. Keys one block ahead and values in two slots
 // otherwise: deeper prefetch measured no faster.
 template <typename T, int D, int V, bool MASK, int SHAPE>
@@ -1205,7 +1262,8 @@ constexpr SdpaKernelFn mfma_kernel() {
   } else {
     // Keys in LDS with loader waves (sdpa_loaders: the host launches 8 waves).
     constexpr bool KLS = sdpa_loaders(D, V, SHAPE, MASK);
-    return sdpa_mfma_kernel<T, D, V, 1, KLS ? 0 : PK, KLS ? 3 : 2, WS, MK, KLS, KLS ? kWaves : 0>;
+    return sdpa_mfma_kernel<T, D, V, 1, KLS ? 0 : PK, KLS ? sdpa_loader_slots(D, V, WS) : 2, WS, MK, KLS,
+                            KLS ? kWaves : 0>;
   }
 }
 
