@@ -564,11 +564,39 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
         }
       }
   };
+  // Values of slot `slot` transposed for the P.V products (issued only;
+  // update() waits for them).
+  using VA_t = u32x2_t[NB][2];
+  auto vread = [&](int slot, VA_t& va) __attribute__((always_inline)) {
+    uint4* const vslot = arr(slot) + wslot + C::KSLOT;
+#pragma unroll
+    for (int db = 0; db < NB; db++) {
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        // V^T block (dims 16db .., keys 16kt + 4g ..): lane r16 addresses key
+        // 16kt + 4g + r16 / 4 at dim col and receives V[16kt + 4g + t][16db + r16].
+        const int kr = 16 * kt + 4 * g + (r16 >> 2);
+        const int col = 16 * db + 4 * (r16 & 3);
+        const int chunk = C::vchunk_lds(kr, col >> 3);
+        const int off = (kr * VCH + chunk) * 16 + (col & 7) * 2;
+        if constexpr (C::ASM_TR) {
+          va[db][kt] = ds_read_tr((uint32_t)(uintptr_t)(lds_void_t*)vslot + off);
+        } else {
+          va[db][kt] = __builtin_bit_cast(
+              u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                           (lds_i16x4_t*)(reinterpret_cast<char*>(vslot) + off)));
+        }
+      }
+    }
+  };
   // Block blk of this chain given its scores: online softmax, rescale, and
-  // o += P . V with the values in value slot `slot`.
+  // o += P . V with the values in value slot `slot`, read into va here or,
+  // VPRE, already issued by the caller (asm LDS reads only).
   constexpr int MKCT = MK ? CT : 1;
-  auto update = [&](const f32x4_t (&sc)[CT][2], const unsigned short (&mk)[MKCT][8], int slot,
-                    int64_t blk) __attribute__((always_inline)) {
+  auto update = [&](auto vpre, const f32x4_t (&sc)[CT][2], const unsigned short (&mk)[MKCT][8],
+                    int slot, int64_t blk, VA_t& va) __attribute__((always_inline)) {
+    constexpr bool VPRE = decltype(vpre)::value;
+    static_assert(!VPRE || C::ASM_TR, "values read ahead by asm reads only");
     // Key indices fit in 32 bits (the host checks N < 2^31).
     const int key0 = (int)blk * kBlk + 4 * g;
     uint2 ph[CT][2], pl[CT][2];
@@ -648,27 +676,7 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
     // order: at most VWAIT younger operations may still be in flight).
     if constexpr (!KL) __builtin_amdgcn_s_waitcnt(wait_vm(C::VWAIT));
     asm volatile("" ::: "memory");
-    uint4* const vslot = arr(slot) + wslot + C::KSLOT;
-    u32x2_t va[NB][2];
-#pragma unroll
-    for (int db = 0; db < NB; db++) {
-#pragma unroll
-      for (int kt = 0; kt < 2; kt++) {
-        // V^T block (dims 16db .., keys 16kt + 4g ..): lane r16 addresses key
-        // 16kt + 4g + r16 / 4 at dim col and receives V[16kt + 4g + t][16db + r16].
-        const int kr = 16 * kt + 4 * g + (r16 >> 2);
-        const int col = 16 * db + 4 * (r16 & 3);
-        const int chunk = C::vchunk_lds(kr, col >> 3);
-        const int off = (kr * VCH + chunk) * 16 + (col & 7) * 2;
-        if constexpr (C::ASM_TR) {
-          va[db][kt] = ds_read_tr((uint32_t)(uintptr_t)(lds_void_t*)vslot + off);
-        } else {
-          va[db][kt] = __builtin_bit_cast(
-              u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                           (lds_i16x4_t*)(reinterpret_cast<char*>(vslot) + off)));
-        }
-      }
-    }
+    if constexpr (!VPRE) vread(slot, va);
     if constexpr (C::ASM_TR) {
       // All of them have returned; the empty statements make every use of a
       // read's result come after the wait.
@@ -729,7 +737,8 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
     }
     f32x4_t sc[CT][2];
     scores(kr, kl, sc);
-    update(sc, mk, slot, blk);
+    VA_t va;
+    update(std::false_type{}, sc, mk, slot, blk, va);
   };
 
   // Block i of the chain: keys loaded at step i - PK, values at step
@@ -756,7 +765,13 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
         // are never used.
         KL_t kl;
         kread(u, kl);
-        if (j >= 1 && j <= nit) update(sp, kr[0].m, (u + SV - 1) % SV, wave + kWaves * (j - 1));
+        if (j >= 1 && j <= nit) {
+          // Block j - 1's values are read before its softmax, which hides
+          // their latency.
+          VA_t va;
+          vread((u + SV - 1) % SV, va);
+          update(std::true_type{}, sp, kr[0].m, (u + SV - 1) % SV, wave + kWaves * (j - 1), va);
+        }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         scores(kr[0], kl, sp);
       }
