@@ -1101,7 +1101,9 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
 #pragma unroll
       for (int i = 0; i < NQ; i++)
         sc[0] = mma32(T(0), __builtin_bit_cast(uint4, kl[0][i]), qt[i], sc[0]);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // sc[0] as an operand keeps the first half's MFMAs ahead of this wait
+      // (the compiler does not order MFMAs against asm statements otherwise).
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sc[0]) :: "memory");
 #pragma unroll
       for (int i = 0; i < NQ; i++) asm volatile("" : "+v"(kl[1][i]));
       sc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
