@@ -142,6 +142,28 @@ def test_short_contexts_through_the_loader_wave_shapes(cuda):
                         assert np.array_equal(bits(y), bits(want.contiguous())), case
 
 
+def test_long_contexts_through_the_loader_wave_shapes(cuda):
+    """The dim-split shapes with loader waves run their chains as a pipeline
+    (a step scores block j while it finishes block j - 1, four slots per wave
+    at dim split 4 and 8; one block per step at dim split 2). Over 8192 keys
+    (65 steps per chain) and 4099 keys (chains of unequal length, a ragged
+    last block), each of them forced gives the one-tile shape's bits,
+    without a mask, end-aligned causal and with sinks."""
+    H, Hkv, D = 32, 8, 128
+    for dname, dtype in LOW:
+        for N in (8192, 4099):
+            q = rn((2, H, 1, D), dtype, 401 + N, device=cuda)
+            k = rn((2, Hkv, N, D), dtype, 402 + N, device=cuda)
+            v = rn((2, Hkv, N, D), dtype, 403 + N, device=cuda)
+            sinks = rn((H,), dtype, 404, device=cuda)
+            for spec, sk in ((None, None), ("end", None), (None, sinks)):
+                ref = bits(run(q, k, v, spec, shape=_lib.SDPA_TILE, sinks=sk))
+                for forced in (_lib.SDPA_SPLIT2, _lib.SDPA_SPLIT4, _lib.SDPA_SPLIT8):
+                    d = int((bits(run(q, k, v, spec, shape=forced, sinks=sk)) != ref).sum())
+                    assert d == 0, "%s N=%d %s sinks=%s shape %d: %d differ" % (
+                        dname, N, spec, sk is not None, forced, d)
+
+
 def _oracle_rows(q, k, v, spec, rows, b, dname):
     """float64 and reference-order fp32 results for query rows `rows` of batch
     entry b (every head), each row as a one-row problem."""
