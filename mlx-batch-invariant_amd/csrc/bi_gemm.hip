@@ -36,21 +36,58 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Geometry for an (M, N) output: decode footprints for small M (they stream
 // the weight once, with loader waves keeping the ring full); otherwise the
-// largest footprint that still puts a workgroup on (nearly) every CU. The
-// thresholds come from measurements of this table on MI355X; since every
+// footprint that moves the fewest operand bytes per CU while its tiles still
+// cover (nearly) every CU. The thresholds come from a grid of this table on
+// MI355X (M = 1..256, N = 4096..32000, K = 4096, 11008, 14336); since every
 // geometry computes the same bits, they only move time.
+int pick_geometry_f32(int64_t M, int64_t N) {
+  if (M <= 16) return 0;
+  if (M <= 64) return ceil_div(N, 32) >= 256 ? 5 : 1;
+  if (ceil_div(M, 64) * ceil_div(N, 64) < 64) return 1;
+  // fp32 carries two accumulator chains: the 256 x 128 footprint (12 waves,
+  // at most 168 registers each) is built for 16-bit types only.
+  if (ceil_div(M, 128) * ceil_div(N, 128) >= 160) return 3;
+  return 2;
+}
+
 int pick_geometry(int64_t M, int64_t N, int dtype) {
   // Decode: 16 x 16 tiles in a 64 KB ring, two workgroups per CU, so one
   // workgroup's ramp-up overlaps another's streaming (M = 1: 6.8 TB/s on a
   // 4096 x 32000 weight).
   if (M <= 16) return 0;
-  // 17..64 rows: 64 x 32 tiles (8 waves) once they still fill the CUs.
-  if (M <= 64) return ceil_div(N, 32) >= 256 ? 5 : 1;
+  if (dtype == BI_F32) return pick_geometry_f32(M, N);
+  const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);  // 128 x 128 tiles
+  const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);     // 64 x 64 tiles
+  if (M <= 64) {
+    // 17..64 rows: the widest tile that still covers most CUs (N = 32000,
+    // M = 64: 128 x 128 41 us, 64 x 32 49 us); 16 x 16 tiles for up to 32
+    // rows of a narrow weight, 64 x 16 above.
+    if (t128 >= 160) return 3;
+    if (t64 >= 160) return 2;
+    if (ceil_div(N, 32) >= (M <= 24 ? 256 : 192)) return 5;
+    return M <= 32 ? 0 : 1;
+  }
   // Small outputs (e.g. 256 x 512): 64 x 64 tiles would leave most CUs idle.
-  if (ceil_div(M, 64) * ceil_div(N, 64) < 64) return 1;
-  // fp32 carries two accumulator chains: the 256 x 128 footprint (12 waves,
-  // at most 168 registers each) is built for 16-bit types only.
-  if (dtype != BI_F32 && ceil_div(M, 256) * ceil_div(N, 128) >= 200) return 4;
+  if (t64 < 64) return 1;
+  if (M <= 128) {
+    // 65..128 rows: 128 x 128 tiles on wide weights (a 256-row tile would be
+    // mostly padding), 64 x 32 on narrow ones.
+    if (t128 >= 80) return 3;
+    return t64 >= 192 ? 2 : 5;
+  }
+  // 256 x 128 once its tiles cover most CUs (N = 22016, M = 192: 45 us
+  // against 56 us for 128 x 128); for M > 256 it must fill them.
+  if (ceil_div(M, 256) * ceil_div(N, 128) >= (M <= 256 ? 160 : 200)) return 4;
+  if (t128 >= 160) return 3;
+  return 2;
+}
+
+// The quantized kernel's footprints: 16 x 16 for decode, 64 x 16 for 17..64
+// rows and small outputs, 128 x 128 where 128-row tiles cover most CUs,
+// else 64 x 64 (its dequantizing operand staging was tuned on these).
+int pick_qgeometry(int64_t M, int64_t N) {
+  if (M <= 16) return 0;
+  if (M <= 64 || ceil_div(M, 64) * ceil_div(N, 64) < 64) return 1;
   if (ceil_div(M, 128) * ceil_div(N, 128) >= 160) return 3;
   return 2;
 }
@@ -280,12 +317,8 @@ extern "C" int bi_qgemm(const void* x, const void* w, const void* scales, const 
                         int dtype, void* hip_stream) {
   const int rc = qvalidate(x, w, scales, biases, out, M, N, K, group_size, bits, dtype);
   if (rc != BI_OK || M == 0 || N == 0) return rc;
-  // The 256 x 128 footprint needs more registers with the dequantizing
-  // loads in flight; 128 x 128 takes its place.
-  int g = pick_geometry(M, N, dtype);
-  if (g == 4) g = 3;
-  if (g == 5) g = 1;  // the quantized kernel keeps 64 x 16 for 17..64 rows
-  return qlaunch(x, w, scales, biases, out, M, N, K, group_size, bits, dtype, g, hip_stream);
+  return qlaunch(x, w, scales, biases, out, M, N, K, group_size, bits, dtype,
+                 pick_qgeometry(M, N), hip_stream);
 }
 
 extern "C" int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,

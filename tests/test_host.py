@@ -61,8 +61,12 @@ def test_footprint_policy():
         return geos[L.bi_gemm_pick_geometry(M, N, 4096, dtype, 1)]
 
     assert pick(1, 4096) == pick(16, 32000) == (16, 16, 4)      # decode
-    assert pick(32, 11008) == pick(64, 32000) == (64, 32, 8)    # 17..64 rows, wide weight
-    assert pick(32, 4096) == (64, 16, 4)                        # 17..64 rows, narrow weight
+    assert pick(32, 4096) == (16, 16, 4)                        # 17..32 rows, narrow weight
+    assert pick(48, 4096) == (64, 16, 4)                        # 33..64 rows, narrow weight
+    assert pick(48, 8192) == pick(96, 4096) == (64, 32, 8)
+    assert pick(32, 11008) == pick(96, 8192) == (64, 64, 8)
+    assert pick(64, 32000) == pick(96, 11008) == (128, 128, 8)  # wide weights, 17..128 rows
+    assert pick(192, 22016) == (256, 128, 12)
     assert pick(256, 512) == (64, 16, 4)                        # small output
     assert pick(256, 4096) == (64, 64, 8)
     assert pick(256, 11008) == (128, 128, 8)
