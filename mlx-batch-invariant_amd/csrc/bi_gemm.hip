@@ -75,11 +75,29 @@ int pick_geometry(int64_t M, int64_t N, int dtype) {
     if (t128 >= 80) return 3;
     return t64 >= 192 ? 2 : 5;
   }
-  // 256 x 128 once its tiles cover most CUs (N = 22016, M = 192: 45 us
-  // against 56 us for 128 x 128); for M > 256 it must fill them.
-  if (ceil_div(M, 256) * ceil_div(N, 128) >= (M <= 256 ? 160 : 200)) return 4;
-  if (t128 >= 160) return 3;
-  return 2;
+  if (M <= 256) {
+    // 256 x 128 once its tiles cover most CUs (N = 22016, M = 192: 45 us
+    // against 56 us for 128 x 128).
+    if (ceil_div(N, 128) >= 160) return 4;
+    return t128 >= 160 ? 3 : 2;
+  }
+  // More rows: the least estimated time per CU, in whole rounds of 256
+  // workgroups (a few tiles past a multiple of the CU count cost a round:
+  // N = 11008, M = 768 takes 95 us in 258 tiles of 256 x 128 and 87 us in
+  // 516 of 128 x 128) times the rows and columns a tile streams, weighted
+  // per footprint (time per streamed row, x1000, measured at M = 4096).
+  struct Cand { int g, bm, bn, w; };
+  constexpr Cand kCands[] = {{2, 64, 64, 129}, {3, 128, 128, 136}, {4, 256, 128, 144}};
+  int best = 2;
+  int64_t best_cost = -1;
+  for (const Cand& c : kCands) {
+    const int64_t cost = ceil_div(ceil_div(M, c.bm) * ceil_div(N, c.bn), 256) * (c.bm + c.bn) * c.w;
+    if (best_cost < 0 || cost < best_cost) {
+      best = c.g;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 // The quantized kernel's footprints: 16 x 16 for decode, 64 x 16 for 17..64

@@ -67,6 +67,11 @@ def test_footprint_policy():
     assert pick(32, 11008) == pick(96, 8192) == (64, 64, 8)
     assert pick(64, 32000) == pick(96, 11008) == (128, 128, 8)  # wide weights, 17..128 rows
     assert pick(192, 22016) == (256, 128, 12)
+    # Whole rounds of 256 workgroups: 172 tiles of 256 x 128 fit one round
+    # (M = 384), 258 need two, where 516 of 128 x 128 need three (M = 768).
+    assert pick(384, 11008) == (256, 128, 12)
+    assert pick(768, 11008) == (128, 128, 8)
+    assert pick(4096, 4096) == pick(4096, 11008) == (256, 128, 12)
     assert pick(256, 512) == (64, 16, 4)                        # small output
     assert pick(256, 4096) == (64, 64, 8)
     assert pick(256, 11008) == (128, 128, 8)
