@@ -377,10 +377,13 @@ SdpaKernelFn mfma_kernel(int64_t D, int64_t V, int dtype, bool mask, int shape) 
 }
 
 // Prefill (a kv head has more than 16 columns): "shared" for D = V = 128
-// without an array mask when its grid of 128-column workgroups gives every
-// compute unit two (L = 2048 causal: 113 -> 92 us; at D = 64 and 32, or on
-// smaller grids, it measured slower than rows), else "rows" when that grid
-// fills the compute units. Otherwise one
+// without an array mask when its grid of 128-column workgroups (one per
+// compute unit at a time) covers at least 4/5 of the compute units and fills
+// at least 3/4 of its rounds over them, or gives every compute unit two
+// (L = 2048 causal: 113 -> 88 us; B = 1, 1024 query rows over 4200 keys:
+// rows 166 us, shared 129 us; at 192 workgroups the two tie, at 320 rows
+// wins; at D = 64 and 32 shared measured slower), else "rows" when that
+// grid fills the compute units. Otherwise one
 // column tile, with the output dims split over 2, 4 or 8 workgroups when the
 // grid of column tiles would leave compute units idle: decode, and short
 // chunks of prefill such as 16 query rows.
@@ -388,7 +391,10 @@ int mfma_pick_shape(int64_t D, int64_t V, int64_t ncol, int64_t streams, bool ar
                     int cus) {
   if (ncol > 16 && D == 128 && V == 128 && !array_mask) {
     const int sc = sdpa_shape_columns(D, V, SDPA_SHARED);
-    if (streams * ((ncol + sc - 1) / sc) >= 2 * (int64_t)cus) return SDPA_SHARED;
+    const int64_t w = streams * ((ncol + sc - 1) / sc);
+    const int64_t rounds = (w + cus - 1) / cus;
+    if (w >= 2 * (int64_t)cus || (5 * w >= 4 * (int64_t)cus && 4 * w >= 3 * rounds * cus))
+      return SDPA_SHARED;
   }
   const int rc = sdpa_shape_columns(D, V, SDPA_ROWS);
   if (ncol > 16 && streams * ((ncol + rc - 1) / rc) >= cus) return SDPA_ROWS;

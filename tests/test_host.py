@@ -177,7 +177,11 @@ def test_sdpa_shape_policy():
     assert pick(1, 16) == _lib.SDPA_SPLIT8      # configs[3] chunk of 16 query rows
     assert pick(1, 64) == _lib.SDPA_SPLIT2      # 8 streams x 16 tiles: too few for rows
     assert pick(4, 64) == pick(1, 256) == _lib.SDPA_ROWS  # prefill: rows fill 256 CUs
-    assert pick(2, 513) == _lib.SDPA_ROWS       # 272 shared workgroups: under 2 per CU
+    assert pick(2, 513) == _lib.SDPA_ROWS       # 272 shared workgroups: a second round barely used
+    # Shared runs one workgroup per CU at a time: it takes over once its grid
+    # covers 4/5 of the CUs and fills 3/4 of its rounds.
+    assert pick(1, 768) == pick(1, 1280) == _lib.SDPA_ROWS     # 192 / 320 workgroups
+    assert pick(1, 896) == pick(1, 1024) == pick(1, 1536) == _lib.SDPA_SHARED  # 224, 256, 384
     assert pick(1, 2048) == pick(4, 1024) == _lib.SDPA_SHARED  # D = V = 128, no array mask
     assert pick(1, 2048, mask=_lib.MASK_CAUSAL) == _lib.SDPA_SHARED
     assert pick(1, 2048, mask=_lib.MASK_ARRAY) == _lib.SDPA_ROWS
