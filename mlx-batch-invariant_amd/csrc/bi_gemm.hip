@@ -41,12 +41,24 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // MI355X (M = 1..256, N = 4096..32000, K = 4096, 11008, 14336); since every
 // geometry computes the same bits, they only move time.
 int pick_geometry_f32(int64_t M, int64_t N) {
+  // fp32 runs closer to its (8x lower) MFMA peak, so whole tiles per CU
+  // weigh more than bytes per CU: at M = 256, N = 11008 64 x 64 tiles take
+  // 226 us and 128 x 128 ones (172 of them) 253 us. The 256 x 128 footprint
+  // (12 waves, at most 168 registers each) is not built for fp32's two
+  // accumulator chains.
   if (M <= 16) return 0;
-  if (M <= 64) return ceil_div(N, 32) >= 256 ? 5 : 1;
+  const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
+  if (M <= 64) {
+    if (ceil_div(N, 128) >= 160) return 2;
+    if (ceil_div(N, 64) >= 160) return 1;
+    return M <= 32 ? 0 : 1;
+  }
   if (ceil_div(M, 64) * ceil_div(N, 64) < 64) return 1;
-  // fp32 carries two accumulator chains: the 256 x 128 footprint (12 waves,
-  // at most 168 registers each) is built for 16-bit types only.
-  if (ceil_div(M, 128) * ceil_div(N, 128) >= 160) return 3;
+  if (M <= 128) {
+    if (t128 >= 200) return 3;
+    return ceil_div(M, 64) * ceil_div(N, 32) >= 256 ? 5 : 1;
+  }
+  if (t128 >= (M <= 256 ? 200 : 160)) return 3;
   return 2;
 }
 

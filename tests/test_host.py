@@ -77,6 +77,8 @@ def test_footprint_policy():
     assert pick(256, 11008) == (128, 128, 8)
     assert pick(256, 32000) == (256, 128, 12)                   # the bench's dominant shape
     assert pick(256, 32000, _lib.F32) == (128, 128, 8)          # fp32: registers
+    assert pick(256, 11008, _lib.F32) == (64, 64, 8)            # fp32: whole tiles per CU
+    assert pick(128, 4096, _lib.F32) == (64, 32, 8)
 
 
 def _err():
