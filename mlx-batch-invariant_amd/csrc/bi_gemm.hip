@@ -112,14 +112,24 @@ int pick_geometry(int64_t M, int64_t N, int dtype) {
   return best;
 }
 
-// The quantized kernel's footprints: 16 x 16 for decode, 64 x 16 for 17..64
-// rows and small outputs, 128 x 128 where 128-row tiles cover most CUs,
-// else 64 x 64 (its dequantizing operand staging was tuned on these).
+// The quantized kernel's footprints, from a grid of every footprint over
+// M = 1..512 and N = 4096..32000 (4-bit, group 64): 16 x 16 for decode and
+// for 17..64 rows of a narrow weight; 64 x 64 for 17..64 rows of a wide one
+// (N = 32000, M = 32: 37 us against 86 us for 64 x 16); above that the
+// dense rules, except that 128 x 128 must fill the CUs (its workgroups
+// dequantize twice the columns: N = 11008, M = 256: 64 x 64 61 us, 128 x 128
+// 70 us).
 int pick_qgeometry(int64_t M, int64_t N) {
   if (M <= 16) return 0;
-  if (M <= 64 || ceil_div(M, 64) * ceil_div(N, 64) < 64) return 1;
-  if (ceil_div(M, 128) * ceil_div(N, 128) >= 160) return 3;
-  return 2;
+  const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);
+  const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
+  if (M <= 64) return ceil_div(N, 64) >= 160 ? 2 : 0;
+  if (t64 < 64) return 1;
+  if (M <= 128) {
+    if (t128 >= 160) return 3;
+    return t64 >= 192 ? 2 : 5;
+  }
+  return (M <= 256 ? t128 : ceil_div(N, 128)) >= 200 ? 3 : 2;
 }
 
 int validate(const void* a, const void* b, void* out, int64_t M, int64_t N, int64_t K,
