@@ -176,6 +176,11 @@ def test_sdpa_shape_policy():
     assert pick(16, 1) == _lib.SDPA_SPLIT2
     assert pick(8, 1) == _lib.SDPA_SPLIT4
     assert pick(1, 1) == pick(4, 1) == _lib.SDPA_SPLIT8  # dims over 8 workgroups
+    # Whole rounds of workgroups (a loader-wave split fills a CU, one tile
+    # takes half): B=6 fits 4-way splits in one round, B=12 2-way, B=24 tiles.
+    assert pick(6, 1) == _lib.SDPA_SPLIT4
+    assert pick(12, 1) == _lib.SDPA_SPLIT2
+    assert pick(24, 1) == _lib.SDPA_TILE
     assert pick(1, 16) == _lib.SDPA_SPLIT8      # configs[3] chunk of 16 query rows
     assert pick(1, 64) == _lib.SDPA_SPLIT2      # 8 streams x 16 tiles: too few for rows
     assert pick(4, 64) == pick(1, 256) == _lib.SDPA_ROWS  # prefill: rows fill 256 CUs
