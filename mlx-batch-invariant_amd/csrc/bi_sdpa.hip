@@ -399,28 +399,23 @@ int mfma_pick_shape(int64_t D, int64_t V, int64_t ncol, int64_t streams, bool ar
   const int rc = sdpa_shape_columns(D, V, SDPA_ROWS);
   if (ncol > 16 && streams * ((ncol + rc - 1) / rc) >= cus) return SDPA_ROWS;
   const int64_t tiles = streams * ((ncol + 15) / 16);  // workgroups at one column tile
-  if (sdpa_loaders(D, V, SDPA_SPLIT2, array_mask)) {
-    // The dim splits with loader waves fill a CU's LDS (one workgroup per
-    // CU at a time), the one-tile shape takes two: the fewest rounds of
-    // workgroups over the CUs, then the most workgroups per column tile.
-    // Half-used rounds cost a whole one (decode B=6, N=8192: 8-way split in
-    // 384 workgroups 68 us, 4-way in 192 37 us; B=24: 2-way 156 us, one
-    // tile 137 us).
-    int best = SDPA_TILE;
-    int64_t best_rounds = (tiles + 2 * (int64_t)cus - 1) / (2 * (int64_t)cus);
-    for (int s = SDPA_SPLIT2; s <= SDPA_SPLIT8; s++) {
-      const int64_t r = ((tiles << (s - 1)) + cus - 1) / cus;
-      if (r <= best_rounds) {
-        best = s;
-        best_rounds = r;
-      }
+  // The fewest rounds of workgroups over the CUs, counting one dim-split
+  // workgroup and two one-tile workgroups per CU at a time, then the most
+  // workgroups per column tile. A half-used round costs a whole one (decode
+  // B=6, N=8192, D=128: 8-way split in 384 workgroups 68 us, 4-way in 192
+  // 37 us; B=24: 2-way 156 us, one tile 137 us; the same at D=64 and 256
+  // and with an array mask).
+  int best = SDPA_TILE;
+  int64_t best_rounds = (tiles * sdpa_shape_splits(V, SDPA_TILE) + 2 * (int64_t)cus - 1) /
+                        (2 * (int64_t)cus);
+  for (int s = SDPA_SPLIT2; s <= SDPA_SPLIT8; s++) {
+    const int64_t r = (tiles * sdpa_shape_splits(V, s) + cus - 1) / cus;
+    if (r <= best_rounds) {
+      best = s;
+      best_rounds = r;
     }
-    return best;
   }
-  if (tiles >= cus) return SDPA_TILE;
-  if (2 * tiles >= cus) return SDPA_SPLIT2;
-  if (4 * tiles >= cus) return SDPA_SPLIT4;
-  return SDPA_SPLIT8;
+  return best;
 }
 
 bool dims_built(int64_t D, int64_t V) {
