@@ -62,14 +62,19 @@ int pick_geometry_f32(int64_t M, int64_t N) {
   return 2;
 }
 
-int pick_geometry(int64_t M, int64_t N, int dtype) {
-  // Decode: 16 x 16 tiles in a 64 KB ring, two workgroups per CU, so one
-  // workgroup's ramp-up overlaps another's streaming (M = 1: 6.8 TB/s on a
-  // 4096 x 32000 weight).
-  if (M <= 16) return 0;
-  if (dtype == BI_F32) return pick_geometry_f32(M, N);
+int pick_geometry(int64_t M, int64_t N, int dtype, int trans_b) {
   const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);  // 128 x 128 tiles
   const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);     // 64 x 64 tiles
+  // Decode: 16 x 16 tiles in a 64 KB ring, two workgroups per CU, so one
+  // workgroup's ramp-up overlaps another's streaming (M = 1: 6.8 TB/s on a
+  // 4096 x 32000 (N, K) weight). A (K, N) weight gives a 16-column tile 32
+  // bytes of each weight row, so wide ones take wider tiles (N = 32000,
+  // M = 1: 128 x 128 40 us, 16 x 16 52 us).
+  if (M <= 16) {
+    if (trans_b || dtype == BI_F32) return 0;
+    return t128 >= 160 ? 3 : t64 >= 160 ? 2 : 0;
+  }
+  if (dtype == BI_F32) return pick_geometry_f32(M, N);
   if (M <= 64) {
     // 17..64 rows: the widest tile that still covers most CUs (N = 32000,
     // M = 64: 128 x 128 41 us, 64 x 32 49 us); 16 x 16 tiles for up to 32
@@ -172,7 +177,7 @@ VecFlags vec_flags(const void* a, const void* b, int64_t N, int64_t K, int dtype
 // The geometry bi_gemm launches: pick_geometry's, unless that one takes
 // aligned operands only and these are not; then the 128 x 128 footprint.
 int pick_for(const void* a, const void* b, int64_t M, int64_t N, int64_t K, int dtype, int trans_b) {
-  int g = pick_geometry(M, N, dtype);
+  int g = pick_geometry(M, N, dtype, trans_b);
   if (kGeometries[g].pl) {
     const VecFlags v = vec_flags(a, b, N, K, dtype, trans_b, kGeometries[g]);
     if (!(v.a && v.b)) g = 3;
@@ -252,8 +257,7 @@ extern "C" int bi_gemm_geometry_info(int g, int* block_m, int* block_n, int* wav
 
 extern "C" int bi_gemm_pick_geometry(int64_t M, int64_t N, int64_t K, int dtype, int trans_b) {
   (void)K;
-  (void)trans_b;
-  return pick_geometry(M, N, dtype);
+  return pick_geometry(M, N, dtype, trans_b);
 }
 
 extern "C" int bi_gemm_with_geometry(const void* a, const void* b, const void* bias, void* out,

@@ -57,10 +57,15 @@ def test_footprint_policy():
     L = _lib.lib()
     geos = bi.geometries()
 
-    def pick(M, N, dtype=_lib.BF16):
-        return geos[L.bi_gemm_pick_geometry(M, N, 4096, dtype, 1)]
+    def pick(M, N, dtype=_lib.BF16, trans_b=1):
+        return geos[L.bi_gemm_pick_geometry(M, N, 4096, dtype, trans_b)]
 
     assert pick(1, 4096) == pick(16, 32000) == (16, 16, 4)      # decode
+    # A (K, N) weight gives a 16-column tile 32 bytes per row: wide ones
+    # take wider tiles at decode sizes too.
+    assert pick(1, 32000, trans_b=0) == (128, 128, 8)
+    assert pick(1, 11008, trans_b=0) == (64, 64, 8)
+    assert pick(1, 4096, trans_b=0) == (16, 16, 4)
     assert pick(32, 4096) == (16, 16, 4)                        # 17..32 rows, narrow weight
     assert pick(48, 4096) == (64, 16, 4)                        # 33..64 rows, narrow weight
     assert pick(48, 8192) == pick(96, 4096) == (64, 32, 8)
