@@ -13,6 +13,7 @@ in that order depends on the number of query rows, the batch, or how far the
 key sequence extends past the keys a row can see.
 """
 
+import ctypes
 import math
 
 import torch
@@ -69,11 +70,18 @@ def _mask_args(mask, B, H, qL, N, dtype):
 def _kernel_view(t):
     """t itself if the kernel can read it in place (last dim contiguous, 16-byte
     aligned rows and base), else a contiguous copy."""
-    ce = 16 // t.element_size()
-    if (t.stride(-1) == 1 and all(s % ce == 0 for s in t.stride()[:-1])
-            and t.data_ptr() % 16 == 0):
-        return t
+    if t.data_ptr() % 16 == 0:
+        if t.is_contiguous() and (t.shape[-1] * t.element_size()) % 16 == 0:
+            return t
+        ce = 16 // t.element_size()
+        st = t.stride()
+        if st[-1] == 1 and all(s % ce == 0 for s in st[:-1]):
+            return t
     return t.contiguous()
+
+
+_NO_MASK_STRIDES = _lib.i64_array((0, 0, 0))
+_I64x9 = ctypes.c_int64 * 9
 
 
 def _sdpa(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks):
@@ -99,12 +107,12 @@ def _sdpa_eager(q, k, v, scale, mask_mode, mask, mstrides, causal_offset, sinks,
     if out.numel() == 0:
         return out
     q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
-    strides = _lib.i64_array([q.stride(0), q.stride(1), q.stride(2),
-                              k.stride(0), k.stride(1), k.stride(2),
-                              v.stride(0), v.stride(1), v.stride(2)])
+    qs, ks, vs = q.stride(), k.stride(), v.stride()
+    strides = _I64x9(qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2])
     L = _lib.lib()
+    ms = _NO_MASK_STRIDES if mask is None else _lib.i64_array(mstrides)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(),
-            mask.data_ptr() if mask is not None else None, _lib.i64_array(mstrides),
+            mask.data_ptr() if mask is not None else None, ms,
             sinks.data_ptr() if sinks is not None else None, out.data_ptr(),
             B, H, Hkv, qL, N, D, V, strides, float(scale), int(mask_mode),
             int(causal_offset), _lib.DTYPE_CODES[q.dtype])
@@ -173,9 +181,10 @@ def scaled_dot_product_attention(q, k, v, *, scale=None, mask=None, sinks=None):
         if tuple(sinks.shape) != (H,):
             raise ValueError("sinks must have shape (%d,), got %s" % (H, tuple(sinks.shape)))
         sinks = sinks.to(q.dtype).contiguous()
-    devs = [q, k, v] + ([m] if m is not None else []) + ([sinks] if sinks is not None else [])
-    for t in devs:
-        if t.device.type != "cuda" or t.device != q.device:
-            raise ValueError("batch-invariant kernels run on the GPU; all operands must be "
-                             "on one cuda device")
+    dev = q.device
+    devs = (q, k, v) if m is None and sinks is None else \
+        [q, k, v] + ([m] if m is not None else []) + ([sinks] if sinks is not None else [])
+    if not q.is_cuda or any(t.device != dev for t in devs[1:]):
+        raise ValueError("batch-invariant kernels run on the GPU; all operands must be "
+                         "on one cuda device")
     return _sdpa(q, k, v, scale, mode, m, mstrides, N - qL, sinks)
