@@ -7,7 +7,8 @@
  * ("geometries": rows x columns of C per workgroup, waves per workgroup). All
  * of them execute the same per-element arithmetic: the same MFMA instruction
  * on the same K-chunks in the same ascending order, then the same epilogue.
- * bi_gemm picks a geometry from (M, N) alone to fill the GPU. These entry
+ * bi_gemm picks a geometry from (M, N), the element type and the weight
+ * layout (never from the values or the row's position). These entry
  * points let a test run one input through every geometry and compare bits,
  * which is the direct proof that the footprint choice cannot change a result.
  */
