@@ -8,9 +8,8 @@ the sweep, (256, K) bf16 activations ~ N(0, 1) times (K, N) bf16 weights
 ~ N(0, 1/K), seeded. `value` is the step's total flops / wall time, inputs
 resident in HBM. Alongside, on the same run:
   * roofline of the dominant kernel (256 x 4096 x 32000), its average
-    duration over about five evenly spaced timed steps (every step when there
-    are fewer than ten) from HIP events that the launch itself records (the
-    kernel's own start and end timestamps);
+    duration over every other timed step from HIP events that the launch
+    itself records (the kernel's own start and end timestamps);
   * stock torch.matmul (hipBLASLt) on the same inputs, interleaved;
   * the same sweep in f16 and fp32 (fp32 against the 157.3 TFLOP/s fp32
     MFMA peak);
@@ -306,16 +305,17 @@ def main():
     torch.cuda.synchronize()
 
     # Timed region: exactly --steps steps, synchronised on both sides. In
-    # about five evenly spaced steps (every step when there are fewer than
-    # ten) the dominant kernel's launch records its own start and end
-    # timestamps into a pair of HIP events (bi_gemm_timed, same kernel and
-    # arguments as bi.matmul): event markers between the launches would idle
-    # the GPU for several microseconds each and be counted in the kernel's
-    # time, and even the self-timed launch in every step cost about 2 % of
-    # the step (204 against 200 us).
-    stride = max(1, args.steps // 5) if args.steps >= 10 else 1
+    # every other step (every step when there are fewer than four) the
+    # dominant kernel's launch records its own start and end timestamps into
+    # a pair of HIP events (bi_gemm_timed, same kernel and arguments as
+    # bi.matmul): event markers between the launches would idle the GPU for
+    # several microseconds each and be counted in the kernel's time. The
+    # self-timed launch in every step cost about 3 us of a 200 us step, in
+    # every other step about 1 us; single launches vary by a few per cent,
+    # so fewer samples made the average noisy.
+    timed = range(1, args.steps, 2) if args.steps >= 4 else range(args.steps)
     evs = {s: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for s in range(0, args.steps, stride)}
+           for s in timed}
     for e0, e1 in evs.values():  # torch creates the underlying HIP event on its first record
         e0.record()
         e1.record()
