@@ -15,10 +15,11 @@ using bi_gemm_dev::KernelFn;
 
 struct Geometry {
   int bm, bn, waves;
-  bool pl;  // loading waves issue every load; 16-byte aligned operands only
+  bool pl;  // loading waves issue every load, or the ping-pong schedule: 16-byte
+            // aligned operands only
 };
 
-#define BI_GEO_ENTRY(id, bm, bn, wm, wn, nw, kb, ns, pl) {bm, bn, nw, pl != 0},
+#define BI_GEO_ENTRY(id, bm, bn, wm, wn, nw, kb, ns, pl, pp) {bm, bn, nw, pl != 0 || pp != 0},
 constexpr Geometry kGeometries[] = {BI_GEOMETRIES(BI_GEO_ENTRY)};
 #undef BI_GEO_ENTRY
 constexpr int kNumGeometries = sizeof(kGeometries) / sizeof(kGeometries[0]);
@@ -102,9 +103,14 @@ int pick_geometry(int64_t M, int64_t N, int dtype, int trans_b) {
   // workgroups (a few tiles past a multiple of the CU count cost a round:
   // N = 11008, M = 768 takes 95 us in 258 tiles of 256 x 128 and 87 us in
   // 516 of 128 x 128) times the rows and columns a tile streams, weighted
-  // per footprint (time per streamed row, x1000, measured at M = 4096).
+  // per footprint (time per streamed row, x1000, measured at M = 4096). The
+  // 256 x 256 ping-pong footprint halves the operand bytes per product of
+  // 128 x 128 (M = 4096: 1.19-1.33 PFLOP/s against 1.06-1.10 for 256 x 128
+  // on (K, N) weights), but needs tiles for most CUs (M = 2048, N = 4096:
+  // 128 of them, 92 us against 63 us for 256 x 128).
   struct Cand { int g, bm, bn, w; };
-  constexpr Cand kCands[] = {{2, 64, 64, 129}, {3, 128, 128, 136}, {4, 256, 128, 144}};
+  constexpr Cand kCands[] = {
+      {2, 64, 64, 129}, {3, 128, 128, 136}, {4, 256, 128, 144}, {6, 256, 256, 192}};
   int best = 2;
   int64_t best_cost = -1;
   for (const Cand& c : kCands) {

@@ -47,6 +47,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -178,8 +180,10 @@ __device__ inline uint4 buffer_chunk(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // the two chunks to even and odd bank groups (c ^ (r & 7) would give both chunk
 // sets the same 8 bank groups: a 2-way conflict on every read).
 template <int RC>
-__device__ inline int swz_k(int r) {  // [rows][RC >= 8 chunks] tiles
-  return RC >= 16 ? (r & 7) << 1 : r & 7;
+__device__ inline int swz_k(int r) {  // [rows][RC >= 4 chunks] tiles
+  // Rows of 4 chunks (64 bytes): rows r and r + 4 share bank groups, so bit 2
+  // of the row picks the chunk pair.
+  return RC >= 16 ? (r & 7) << 1 : RC == 8 ? r & 7 : ((r >> 2) & 1) << 1;
 }
 // (K, N) B tiles are read with ds_read_b64_tr_b16: lane group g reads k-rows
 // 8g + (0..3) (plus 4 for the second half), 32 bytes each. One pass serves
@@ -229,7 +233,7 @@ struct QSlot {
 };
 
 template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, int QB = 0,
-          bool PL = false>
+          bool PL = false, bool PP = false>
 struct GemmTile {
   static constexpr int NT = 64 * NW;
   static constexpr int CW = WM * WN;                  // compute waves
@@ -249,7 +253,9 @@ struct GemmTile {
   static constexpr int DMA = STAGE_CH / 64 / LDW;     // 1 KB LDS-DMA loads per loading wave per stage
   static constexpr int CHAINS = sizeof(T) == 4 ? 2 : 1;    // fp32: chain per chunk-step parity
   static_assert(CW <= NW && FM >= 1 && FN >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "geometry");
-  static_assert(KB % 128 == 0 && CS % 2 == 0, "stage bytes");
+  // fp32 alternates two chains by chunk-step parity, so its stages hold an
+  // even number of chunk-steps.
+  static_assert(KB % 64 == 0 && CS % CHAINS == 0 && (KB >= 128 || sizeof(T) == 2), "stage bytes");
   static_assert(TB || (NN_CPR >= 1 && (NN_CPR & (NN_CPR - 1)) == 0), "bad (K,N) tile width");
   static constexpr int DMA_A = A_CH / 64 / LDW;     // of which A loads (the rest load B)
   static_assert(LDW >= 1, "PL needs loading waves");
@@ -309,23 +315,28 @@ struct GemmTile {
     return i < DMA_A ? i * LDW + lw : (i - DMA_A) * LDW + lw;
   }
 
-  __device__ __forceinline__ void init_dma() {
+  // Load addressing of 1 KB block `blk` of a stage's A (is_a) or B region:
+  // this lane's panel byte offset for stage 0 and the K index that decides
+  // whether it is inside the operand.
+  __device__ __forceinline__ void dma_addr(bool is_a, int blk, uint32_t& base, int32_t& kidx) const {
     constexpr uint32_t E = sizeof(T);
-#pragma unroll
-    for (int i = 0; i < DMA; i++) {
-      const int p = dma_blk(i) * 64 + lane;  // chunk position within the A or B region
-      if (i < DMA_A || TB) {
-        const int r = p / RC, c = (p % RC) ^ swz_k<RC>(r);
-        dma_base[i] = (uint32_t)(r * K + c * EPC) * E;
-        dma_kidx[i] = c * EPC;
-      } else {
-        const int kr = p / NN_CPR, c = (p % NN_CPR) ^ swz_nn<T, NN_CPR>(kr);
-        const int n = c * EPC;
-        dma_base[i] = (uint32_t)(kr * N + n) * E;
-        // A column outside N never loads: push its K index out of range.
-        dma_kidx[i] = (n0 + n < N) ? kr : INT32_MAX / 2;
-      }
+    const int p = blk * 64 + lane;  // chunk position within the A or B region
+    if (is_a || TB) {
+      const int r = p / RC, c = (p % RC) ^ swz_k<RC>(r);
+      base = (uint32_t)(r * K + c * EPC) * E;
+      kidx = c * EPC;
+    } else {
+      const int kr = p / NN_CPR, c = (p % NN_CPR) ^ swz_nn<T, NN_CPR>(kr);
+      const int n = c * EPC;
+      base = (uint32_t)(kr * N + n) * E;
+      // A column outside N never loads: push its K index out of range.
+      kidx = (n0 + n < N) ? kr : INT32_MAX / 2;
     }
+  }
+
+  __device__ __forceinline__ void init_dma() {
+#pragma unroll
+    for (int i = 0; i < DMA; i++) dma_addr(i < DMA_A, dma_blk(i), dma_base[i], dma_kidx[i]);
   }
 
   // Issue this wave's LDS-DMA loads of stage s into `slot`.
@@ -549,6 +560,230 @@ struct GemmTile {
       dma_rounds<true>(slots, nst, acc);
     else
       dma_rounds<false>(slots, nst, acc);
+  }
+
+  // ---- Ping-pong schedule (PP). The compute waves form two groups, waves
+  // 0 .. CW/2 - 1 and CW/2 .. CW - 1; the hardware places wave w and wave
+  // w + 4 of a workgroup on the same SIMD, so every SIMD holds waves of both
+  // groups (CW/2 a multiple of 4). Chunk-step q takes two phases, separated
+  // by workgroup barriers: group 0 reads q's operands from LDS in phase 2q
+  // and runs q's MFMAs in phase 2q + 1; group 1 does the same one phase
+  // later. In every phase one group's waves issue matrix products while the
+  // other group's read LDS, so a SIMD's matrix core does not wait for its
+  // own waves' operand reads, and each wave holds the operands of one
+  // chunk-step only (16 waves of 64 x 64 wave tiles fit 128 registers). The
+  // MFMAs per element and their order are those of every other footprint.
+  // Loads: every stage holds one chunk-step; group 0 loads the A tiles and
+  // group 1 the B tiles of the stage NS - 1 ahead, each right after issuing
+  // its products (a load issue that stalls on a busy memory pipeline then
+  // delays no operand read and no matrix product).
+  static constexpr int PPG = CW / 2;                            // compute waves per group
+  static constexpr int DMA_PA = PP ? A_CH / 64 / PPG : 1;  // A loads per group-0 wave per stage
+  static constexpr int DMA_PB = PP ? B_CH / 64 / PPG : 1;  // B loads per group-1 wave per stage
+  static constexpr int PPD = DMA_PA > DMA_PB ? DMA_PA : DMA_PB;
+  static_assert(!PP || (!PL && CS == 1 && NS >= 3 && PPG % 4 == 0 && A_CH % (64 * PPG) == 0 &&
+                        B_CH % (64 * PPG) == 0 && PPD * (NS - 2) <= 63),
+                "ping-pong geometry");
+  uint32_t pp_base[PPD];
+  int32_t pp_kidx[PPD];
+
+  __device__ __forceinline__ void init_dma_pp(int grp, int gw) {
+    const int nd = grp == 0 ? DMA_PA : DMA_PB;
+#pragma unroll
+    for (int i = 0; i < PPD; i++)
+      if (i < nd) dma_addr(grp == 0, i * PPG + gw, pp_base[i], pp_kidx[i]);
+  }
+
+  template <bool IS_A>
+  __device__ __forceinline__ void dma_pp(int64_t s, Slot slot, int gw) const {
+    constexpr uint32_t E = sizeof(T);
+    constexpr int ND = IS_A ? DMA_PA : DMA_PB;
+    const int32_t kleft = (int32_t)(K - s * EPS);
+    const uint32_t step = (IS_A || TB) ? (uint32_t)(s * EPS) * E : (uint32_t)(s * EPS * N) * E;
+#pragma unroll
+    for (int i = 0; i < ND; i++) {
+      lds_void_t* dst = (lds_void_t*)((IS_A ? slot.a : slot.b) + (i * PPG + gw) * 64);
+      const uint32_t off = pp_kidx[i] < kleft ? pp_base[i] + step : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(IS_A ? ra_src : rb_src, dst, 16, off, 0, 0, 0);
+    }
+  }
+
+  // Operand reads of the ping-pong schedule, issued as ds_read instructions
+  // from one per-lane byte offset per operand block column plus the slot's
+  // LDS address (a scalar, added right before the reads): the compiler would
+  // otherwise keep a VGPR address per slot and block, which does not fit the
+  // registers of 16 waves. The reads are waited for explicitly
+  // (lgkmcnt(0) before the barrier that closes the read phase); the values
+  // are first used after that barrier.
+  uint32_t pa_off[CS], pb_off[CS][FN];
+
+  __device__ __forceinline__ void init_lds_offsets_pp() {
+#pragma unroll
+    for (int j = 0; j < CS; j++) {
+      pa_off[j] = (uint32_t)((wm * WTM + r16) * RC + ((4 * j + g) ^ swz_k<RC>(r16))) * 16;
+#pragma unroll
+      for (int jn = 0; jn < FN; jn++) {
+        if constexpr (TB) {
+          pb_off[j][jn] =
+              (uint32_t)((wn * WTN + jn * 16 + r16) * RC + ((4 * j + g) ^ swz_k<RC>(r16))) * 16;
+        } else {
+          // As load_b: lane r16 of group g addresses k-row 32 j + 8 g + r16 / 4
+          // at column 4 (r16 % 4) of the block; the second half (4 rows on)
+          // has the same swizzle, so it is an immediate offset.
+          const int kr = 32 * j + 8 * g + (r16 >> 2);
+          const int col = wn * WTN + jn * 16 + 4 * (r16 & 3);
+          const int chunk = (col >> 3) ^ swz_nn<T, NN_CPR>(kr);
+          pb_off[j][jn] = (uint32_t)((kr * NN_CPR + chunk) * 16 + (col & 7) * 2);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ static uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(lds_void_t*)p;
+  }
+
+  __device__ __forceinline__ void read_operands_pp(Slot sl, int j, uint4 (&av)[FM],
+                                                   uint4 (&bv)[FN]) const {
+    static_assert(sizeof(T) == 2, "ping-pong: 16-bit element types");
+    uint32_t aa;
+    asm volatile("v_add_u32 %0, %1, %2" : "=v"(aa) : "s"(lds_addr(sl.a)), "v"(pa_off[j]));
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      u32x4_t v;
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(aa), "n"(i * 16 * RC * 16));
+      av[i] = __builtin_bit_cast(uint4, v);
+    }
+    const uint32_t bs = lds_addr(sl.b);
+#pragma unroll
+    for (int jn = 0; jn < FN; jn++) {
+      uint32_t ba;
+      asm volatile("v_add_u32 %0, %1, %2" : "=v"(ba) : "s"(bs), "v"(pb_off[j][jn]));
+      if constexpr (TB) {
+        u32x4_t v;
+        asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(ba));
+        bv[jn] = __builtin_bit_cast(uint4, v);
+      } else {
+        u32x2_t h0, h1;
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(h0) : "v"(ba));
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(h1) : "v"(ba), "n"(4 * NN_CPR * 16));
+        bv[jn] = make_uint4(h0.x, h0.y, h1.x, h1.y);
+      }
+    }
+  }
+
+  // Waits for this wave's operand reads; tying the registers to the wait
+  // keeps every use after it.
+  __device__ __forceinline__ static void wait_operands(uint4 (&av)[FM], uint4 (&bv)[FN]) {
+    u32x4_t a[FM], b[FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++) a[i] = __builtin_bit_cast(u32x4_t, av[i]);
+#pragma unroll
+    for (int jn = 0; jn < FN; jn++) b[jn] = __builtin_bit_cast(u32x4_t, bv[jn]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      asm volatile("" : "+v"(a[i]));
+      av[i] = __builtin_bit_cast(uint4, a[i]);
+    }
+#pragma unroll
+    for (int jn = 0; jn < FN; jn++) {
+      asm volatile("" : "+v"(b[jn]));
+      bv[jn] = __builtin_bit_cast(uint4, b[jn]);
+    }
+  }
+
+  __device__ __forceinline__ static void pp_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  __device__ __forceinline__ void pp_mfma(const uint4 (&av)[FM], const uint4 (&bv)[FN],
+                                          f32x4_t (&acc)[CHAINS][FM][FN]) const {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int jn = 0; jn < FN; jn++) acc[0][i][jn] = chunk_step(T(0), av[i], bv[jn], acc[0][i][jn]);
+  }
+
+  // One group's rounds (GRP 0 or 1; COMPUTE false for a wave whose sub-tile
+  // lies outside C: it keeps the barriers and its share of the loads). Each
+  // group runs a straight sequence of phases of its own, so its operands and
+  // accumulators stay in the same registers from phase to phase. Phase p
+  // opens with barrier B_p; stage s (= chunk-step s) is first read after
+  // B_2s, and a wave that loads part of it waits for its own loads of it
+  // before that barrier. Group 0 has issued the A tiles of stages up to
+  // s + NS - 2 by then (in phase 2s - 1), group 1 the B tiles of stages up
+  // to s + NS - 3 (in phase 2s - 2; its loads of phase 2s follow B_2s).
+  // Stage s + NS - 1 refills the slot of stage s - 1, whose last reads
+  // (group 1, phase 2s - 1) are complete before B_2s.
+  template <int GRP, bool COMPUTE, typename Slots>
+  __device__ __forceinline__ void pp_rounds(const Slots& slots, int64_t nst, int gw,
+                                            f32x4_t (&acc)[CHAINS][FM][FN]) const {
+    uint4 av[FM], bv[FN];
+    if constexpr (GRP == 1) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DMA_PB * (NS - 2)));
+      pp_barrier();  // B_0: group 0 reads chunk-step 0
+    }
+    for (int64_t s0 = 0; s0 < nst; s0 += NS) {
+#pragma unroll
+      for (int u = 0; u < NS; u++) {
+        if constexpr (GRP == 0) {
+          // B_2s: read chunk-step s; B_2s+1: its products, then load the A
+          // tiles of stage s + NS - 1.
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DMA_PA * (NS - 2)));
+          pp_barrier();
+          if constexpr (COMPUTE) {
+            read_operands_pp(slots(u), 0, av, bv);
+            wait_operands(av, bv);
+          }
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+          pp_barrier();
+          if constexpr (COMPUTE) pp_mfma(av, bv, acc);
+          dma_pp<true>(s0 + u + NS - 1, slots((u + NS - 1) % NS), gw);
+        } else {
+          // B_2s+1: read chunk-step s; B_2s+2: its products, then load the B
+          // tiles of stage s + NS - 1. Stage s + 1's B tiles must have landed
+          // before B_2s+2.
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+          pp_barrier();
+          if constexpr (COMPUTE) {
+            read_operands_pp(slots(u), 0, av, bv);
+            wait_operands(av, bv);
+          }
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DMA_PB * (NS - 3)));
+          pp_barrier();
+          if constexpr (COMPUTE) pp_mfma(av, bv, acc);
+          dma_pp<false>(s0 + u + NS - 1, slots((u + NS - 1) % NS), gw);
+        }
+      }
+    }
+    if constexpr (GRP == 0) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+      pp_barrier();  // B_2Q: group 1's last products
+    }
+  }
+
+  template <typename Slots>
+  __device__ __forceinline__ void main_loop_pp(const Slots& slots, int64_t nst, bool computes,
+                                               f32x4_t (&acc)[CHAINS][FM][FN]) {
+    static_assert(CHAINS == 1, "ping-pong: 16-bit element types");
+    const int grp = wave < PPG ? 0 : 1;
+    const int gw = wave - grp * PPG;
+    init_dma_pp(grp, gw);
+    init_lds_offsets_pp();
+    if (grp == 0) {
+#pragma unroll
+      for (int u = 0; u < NS - 1; u++) dma_pp<true>(u, slots(u), gw);
+      if (computes) pp_rounds<0, true>(slots, nst, gw, acc);
+      else pp_rounds<0, false>(slots, nst, gw, acc);
+    } else {
+#pragma unroll
+      for (int u = 0; u < NS - 1; u++) dma_pp<false>(u, slots(u), gw);
+      if (computes) pp_rounds<1, true>(slots, nst, gw, acc);
+      else pp_rounds<1, false>(slots, nst, gw, acc);
+    }
   }
 
   // ---- Affine-quantized B (QB bits per weight; 16-bit elements only).
@@ -916,9 +1151,10 @@ struct GemmTile {
   }
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, bool PL>
+template <typename T, int BM, int BN, int WM, int WN, int NW, int KB, int NS, bool TB, bool PL,
+          bool PP>
 __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
-  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB, 0, PL>;
+  using Tile = GemmTile<T, BM, BN, WM, WN, NW, KB, NS, TB, 0, PL, PP>;
   constexpr int FM = Tile::FM, FN = Tile::FN, CHAINS = Tile::CHAINS;
   constexpr int AC = Tile::A_CH, BC = Tile::B_CH;
   // The LDS ring: NS stages, each an A and a B array (unused ones are a single chunk).
@@ -979,13 +1215,17 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
   t.init_lds_offsets();
   if (p.vec_a && p.vec_b) {
     t.init_buffers();
-    // With PL only the loading waves need the load addressing.
-    if (!PL || t.wave >= Tile::CW) t.init_dma();
-    t.main_loop_dma(slots, nst, computes, acc);
-  } else if constexpr (!PL) {
-    // PL footprints take 16-byte aligned operands only: the host launches
-    // another footprint for the others (the slow path's registers would make
-    // the whole kernel spill).
+    if constexpr (PP) {
+      t.main_loop_pp(slots, nst, computes, acc);
+    } else {
+      // With PL only the loading waves need the load addressing.
+      if (!PL || t.wave >= Tile::CW) t.init_dma();
+      t.main_loop_dma(slots, nst, computes, acc);
+    }
+  } else if constexpr (!PL && !PP) {
+    // PL and PP footprints take 16-byte aligned operands only: the host
+    // launches another footprint for the others (the slow path's registers
+    // would make the whole kernel spill).
     t.main_loop_slow(slots, nst, nsteps, computes, acc);
   }
 
@@ -998,7 +1238,10 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
   // values.
   constexpr int SWB = Tile::WTM * Tile::WTN * (int)sizeof(T);  // staged bytes per wave
   constexpr int WPA = AC * 16 / SWB;                            // waves per A array
-  constexpr bool STAGED = WPA >= 1 && WPA * NS >= Tile::CW;
+  constexpr int WPB = BC * 16 / SWB;                            // waves per B array
+  // The A arrays of the ring, or where they are too few, A and B arrays.
+  constexpr bool STAGED_A = WPA >= 1 && WPA * NS >= Tile::CW;
+  constexpr bool STAGED = STAGED_A || (WPA >= 1 && (WPA + WPB) * NS >= Tile::CW);
   if constexpr (STAGED) {
     __builtin_amdgcn_s_waitcnt(0);
     asm volatile("s_barrier" ::: "memory");
@@ -1011,7 +1254,14 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(GemmArgs p) {
     const bool whole = wrow + Tile::WTM <= M && wcol + Tile::WTN <= N &&
                        N % Tile::EPC == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
     if (whole) {
-      T* stage = reinterpret_cast<T*>(slots(t.wave / WPA).a) + (t.wave % WPA) * (SWB / (int)sizeof(T));
+      T* stage;
+      if constexpr (STAGED_A) {
+        stage = reinterpret_cast<T*>(slots(t.wave / WPA).a) + (t.wave % WPA) * (SWB / (int)sizeof(T));
+      } else {
+        const int u = t.wave / (WPA + WPB), r = t.wave % (WPA + WPB);
+        stage = r < WPA ? reinterpret_cast<T*>(slots(u).a) + r * (SWB / (int)sizeof(T))
+                        : reinterpret_cast<T*>(slots(u).b) + (r - WPA) * (SWB / (int)sizeof(T));
+      }
 #pragma unroll
       for (int jn = 0; jn < FN; jn++) {
         const int c = jn * 16 + t.r16;
@@ -1138,14 +1388,16 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
 // Footprints of C per workgroup. Every entry runs the same per-element
 // arithmetic; the table only trades parallelism against operand reuse and
 // latency hiding. Columns: id, BM, BN, WM, WN, NW (waves), KB (stage bytes),
-// NS (LDS ring stages), PL (loading waves issue all loads).
-#define BI_GEOMETRIES(X)                  \
-  X(0, 16, 16, 1, 1, 4, 512, 4, 0)        \
-  X(1, 64, 16, 4, 1, 4, 256, 4, 0)        \
-  X(2, 64, 64, 2, 2, 8, 256, 4, 0)        \
-  X(3, 128, 128, 4, 2, 8, 128, 4, 0)      \
-  X(4, 256, 128, 4, 2, 12, 128, 3, 1)     \
-  X(5, 64, 32, 4, 2, 8, 256, 3, 0)
+// NS (LDS ring stages), PL (loading waves issue all loads), PP (ping-pong
+// schedule of the compute waves).
+#define BI_GEOMETRIES(X)                     \
+  X(0, 16, 16, 1, 1, 4, 512, 4, 0, 0)        \
+  X(1, 64, 16, 4, 1, 4, 256, 4, 0, 0)        \
+  X(2, 64, 64, 2, 2, 8, 256, 4, 0, 0)        \
+  X(3, 128, 128, 4, 2, 8, 128, 4, 0, 0)      \
+  X(4, 256, 128, 4, 2, 12, 128, 3, 1, 0)     \
+  X(5, 64, 32, 4, 2, 8, 256, 3, 0, 0)        \
+  X(6, 256, 256, 4, 4, 16, 64, 4, 0, 1)
 
 using KernelFn = void (*)(GemmArgs);
 
@@ -1154,11 +1406,11 @@ template <typename T>
 KernelFn kernel_for(int g, bool trans_b) {
 // fp32 carries two accumulator chains per element: with more than 8 waves
 // (at most 168 registers each) the 64 x 64 wave tiles do not fit.
-#define BI_GEO_CASE(id, bm, bn, wm, wn, nw, kb, ns, pl)                          \
-  case id:                                                                      \
-    if constexpr (sizeof(T) == 4 && nw > 8) return nullptr;                     \
-    else return trans_b ? gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, pl>  \
-                        : gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, false, pl>;
+#define BI_GEO_CASE(id, bm, bn, wm, wn, nw, kb, ns, pl, pp)                             \
+  case id:                                                                             \
+    if constexpr (sizeof(T) == 4 && (nw > 8 || pp)) return nullptr;                    \
+    else return trans_b ? gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, pl, pp>     \
+                        : gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, false, pl, pp>;
   switch (g) { BI_GEOMETRIES(BI_GEO_CASE) }
 #undef BI_GEO_CASE
   return nullptr;
@@ -1180,9 +1432,9 @@ KernelFn qkernel_gs(int group) {
 
 template <typename T>
 KernelFn qkernel_for(int g, int bits, int group) {
-#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns, pl)                            \
+#define BI_QGEO_CASE(id, bm, bn, wm, wn, nw, kb, ns, pl, pp)                         \
   case id:                                                                          \
-    if constexpr (bm * bn <= 128 * 128 && !pl) {                                    \
+    if constexpr (bm * bn <= 128 * 128 && !pl && !pp) {                             \
       switch (bits) {                                                               \
         case 2: return qkernel_gs<T, bm, bn, wm, wn, nw, kb, 2>(group);             \
         case 4: return qkernel_gs<T, bm, bn, wm, wn, nw, kb, 4>(group);             \

@@ -9,10 +9,6 @@ import numpy as np
 PRECISION = {"float32": 24, "float16": 11, "bfloat16": 8}
 
 
-def dtype_name(t):
-    return str(t.dtype).replace("torch.", "")
-
-
 def bits(t):
     """Raw bit patterns of a torch tensor as a flat numpy uint array.
 

@@ -134,6 +134,35 @@ def test_all_geometries_agree(cuda, trans_b):
     assert {gi for gi, dn in ran if dn != "float32"} == set(range(len(geos)))
 
 
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_large_footprints_agree(cuda, trans_b):
+    """The large-M footprints (128 x 128, 256 x 128 with loading waves, 256 x
+    256 ping-pong) over several rounds of workgroups, with ragged M, N and K
+    tails and a partial group of row blocks, give the same bits; at M = 4096
+    bi_gemm picks 256 x 256 and a row keeps its M = 1 bits there."""
+    geos = _gemm.geometries()
+    big = [geos.index(f) for f in ((128, 128, 8), (256, 128, 12), (256, 256, 16))]
+    for dname, dtype in DTYPES[1:]:
+        M, K, N = 4360, 1032, 4104
+        a = rn((M, K), dtype, 41, device=cuda)
+        b = rn((N, K) if trans_b else (K, N), dtype, 42, std=K ** -0.5, device=cuda)
+        c = rn((N,), dtype, 43, device=cuda)
+        outs = [bits(_gemm._gemm(a, b, c, trans_b, 0.75, -1.5, geometry=g)) for g in big]
+        for g, o in zip(big[1:], outs[1:]):
+            d = int((o != outs[0]).sum())
+            assert d == 0, "%s trans_b=%s geometry %s: %d differ" % (dname, trans_b, geos[g], d)
+        M, N = 4096, 4096
+        a = rn((M, K), dtype, 44, device=cuda)
+        b = rn((N, K) if trans_b else (K, N), dtype, 45, std=K ** -0.5, device=cuda)
+        from mlx_batch_invariant import _lib
+        assert geos[_lib.lib().bi_gemm_pick_geometry(M, N, K, _lib.DTYPE_CODES[dtype],
+                                                     int(trans_b))] == (256, 256, 16)
+        y = bits(_gemm._gemm(a, b, None, trans_b)).reshape(M, N)
+        for r in (0, 1, 2047, 4095):
+            one = bits(_gemm._gemm(a[r:r + 1].contiguous(), b, None, trans_b))
+            assert (y[r] == one).all(), "%s trans_b=%s row %d" % (dname, trans_b, r)
+
+
 def test_unaligned_operands_leave_the_aligned_only_footprint(cuda):
     """The 256x128 footprint (its loading waves issue every load) takes
     16-byte aligned operands only: forcing it on others raises, and bi_gemm
