@@ -54,6 +54,8 @@ CPU_ROWS = 256              # rows of M per shape in the CPU sample (all of them
 CPU_SECONDS = 10.0          # repeat whole passes until at least this long
 CPU_SDPA_B = 4              # batch entries of configs[2] in the CPU attention sample
 CPU_SDPA_SECONDS = 5.0
+SUSTAINED_S = 1.5           # seconds of repeated steps in the sustained leg
+PREFILL_M = 4096            # rows of the configs[4] prefill GEMMs (batch 8 x 512 tokens)
 
 
 def gemm_flops(m, k, n):
@@ -209,6 +211,101 @@ def cpu_sdpa_baseline(torch, np):
             "torch_cpu_gbps": round(by * tpasses / tdt / 1e9, 3)}
 
 
+def graph_us(torch, fn, calls=20, replays=7):
+    """Device time of one fn() call: `calls` calls captured in a HIP graph,
+    replayed `replays` times between HIP events; median replay / calls."""
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3 / calls)
+    del graph
+    return statistics.median(times)
+
+
+def prefill_gemms(torch, bi, dev, steps=8, warmup=3):
+    """configs[4]'s prefill GEMMs at batch 8 x 512 tokens (M = 4096 rows),
+    bi.linear on (N, K) weights, bf16: one step runs the four (K, N) shapes of
+    the sweep in turn (474 MB of weights, more than the Infinity Cache), each
+    bi launch timed by its own timestamps and each stock F.linear (hipBLASLt)
+    by HIP events, inside the steps. MFMA-bound: fractions of the 2.5 PFLOP/s
+    dense bf16 peak."""
+    from mlx_batch_invariant import _gemm
+
+    g = torch.Generator().manual_seed(5)
+    Mp = PREFILL_M
+    ops = []
+    for K, N in SHAPES[1:]:
+        x = torch.randn(Mp, K, generator=g).to(torch.bfloat16).to(dev)
+        w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(dev)
+        ops.append((K, N, x, w))
+    ev = lambda: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    bi_ev = [[ev() for _ in ops] for _ in range(steps)]
+    st_ev = [[ev() for _ in ops] for _ in range(steps)]
+    for row in bi_ev + st_ev:
+        for e0, e1 in row:
+            e0.record()
+            e1.record()
+    torch.cuda.synchronize()
+    for s_ in range(warmup + steps):
+        for i, (K, N, x, w) in enumerate(ops):
+            if s_ >= warmup:
+                _gemm.linear_timed(x, w, *bi_ev[s_ - warmup][i])
+            else:
+                bi.linear(x, w)
+        for i, (K, N, x, w) in enumerate(ops):
+            if s_ >= warmup:
+                e0, e1 = st_ev[s_ - warmup][i]
+                e0.record()
+                torch.nn.functional.linear(x, w)
+                e1.record()
+            else:
+                torch.nn.functional.linear(x, w)
+    torch.cuda.synchronize()
+    shapes, tot_fl, tot_bi, tot_st = [], 0.0, 0.0, 0.0
+    for i, (K, N, x, w) in enumerate(ops):
+        tb = statistics.median(bi_ev[s_][i][0].elapsed_time(bi_ev[s_][i][1]) * 1e3
+                               for s_ in range(steps))
+        ts = statistics.median(st_ev[s_][i][0].elapsed_time(st_ev[s_][i][1]) * 1e3
+                               for s_ in range(steps))
+        fl = gemm_flops(Mp, K, N)
+        tot_fl, tot_bi, tot_st = tot_fl + fl, tot_bi + tb, tot_st + ts
+        shapes.append({"M": Mp, "K": K, "N": N, "bi_us": round(tb, 1),
+                       "bi_tflops": round(fl / tb / 1e6, 1),
+                       "mfma_frac": round(fl / tb / 1e6 / PEAK_BF16_TFLOPS, 4),
+                       "stock_us": round(ts, 1), "stock_tflops": round(fl / ts / 1e6, 1),
+                       "stock_mfma_frac": round(fl / ts / 1e6 / PEAK_BF16_TFLOPS, 4),
+                       "geometry": _gemm.geometries()[
+                           _gemm._lib.lib().bi_gemm_pick_geometry(Mp, N, K, 2, 1)]})
+    del ops
+    torch.cuda.empty_cache()
+    return {"config": "configs[4] prefill GEMMs: M=%d (batch 8 x 512 tokens), bi.linear (N,K) "
+                      "weights, bf16, the four (K,N) shapes of the sweep per step" % Mp,
+            "steps_timed": steps, "shapes": shapes,
+            "bi_tflops": round(tot_fl / tot_bi / 1e6, 1),
+            "mfma_frac": round(tot_fl / tot_bi / 1e6 / PEAK_BF16_TFLOPS, 4),
+            "stock_tflops": round(tot_fl / tot_st / 1e6, 1),
+            "stock_mfma_frac": round(tot_fl / tot_st / 1e6 / PEAK_BF16_TFLOPS, 4)}
+
+
 def model_determinism(torch, bi, dev):
     """random-init 32-layer Llama-shaped decoder, 512-token seeded
     prompt; bits of sequence 0's last-position logits at batch 8 vs batch 1,
@@ -333,6 +430,31 @@ def main():
     value = step_flops * args.steps / elapsed / 1e12
     dom_us = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs.values()) * 1e3
 
+    # Sustained: the same step repeated for at least SUSTAINED_S seconds (the
+    # burst above covers a few milliseconds; the dominant kernel slows by
+    # several per cent under longer load), the dominant launch self-timed in
+    # every 16th step.
+    n_sus = max(args.steps, int(math.ceil(SUSTAINED_S * 1e3 / ms_per_step)))
+    sus_timed = list(range(8, n_sus, 16))
+    sus_evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in sus_timed]
+    for e0, e1 in sus_evs:
+        e0.record()
+        e1.record()
+    torch.cuda.synchronize()
+    sus_map = dict(zip(sus_timed, sus_evs))
+    t0 = time.perf_counter()
+    for s_ in range(n_sus):
+        for i, (_, _, a, w) in enumerate(ops):
+            if i == dom and s_ in sus_map:
+                _gemm.matmul_timed(a, w, *sus_map[s_])
+            else:
+                bi.matmul(a, w)
+    torch.cuda.synchronize()
+    sus_elapsed = time.perf_counter() - t0
+    sus_us = [e0.elapsed_time(e1) * 1e3 for e0, e1 in sus_evs]
+    q4 = sus_us[len(sus_us) * 3 // 4:]
+
     # Per-shape and stock comparison (HIP events, interleaved A/B, median of 9).
     def time_us(fn, reps=20):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -397,7 +519,15 @@ def main():
             "mfma_achieved_tflops": round(fl / dom_us / 1e6, 1),
             "mfma_frac": round(fl / dom_us / 1e6 / PEAK_BF16_TFLOPS, 4),
             "frac_of_min_roof": round((fl / dom_us / 1e6) /
-                                      min(PEAK_BF16_TFLOPS, fl / by * PEAK_HBM_GBS / 1e3), 4)}
+                                      min(PEAK_BF16_TFLOPS, fl / by * PEAK_HBM_GBS / 1e3), 4),
+            "sustained": {"seconds": round(sus_elapsed, 2), "steps": n_sus,
+                          "value_tflops": round(step_flops * n_sus / sus_elapsed / 1e12, 2),
+                          "avg_launch_us": round(statistics.mean(sus_us), 2),
+                          "frac": round(by / statistics.mean(sus_us) / 1e3 / PEAK_HBM_GBS, 4),
+                          "last_quarter_avg_launch_us": round(statistics.mean(q4), 2),
+                          "last_quarter_frac": round(by / statistics.mean(q4) / 1e3 /
+                                                     PEAK_HBM_GBS, 4),
+                          "launches_timed": len(sus_us)}}
 
     # Decode SDPA.
     g = torch.Generator().manual_seed(0)
@@ -436,6 +566,22 @@ def main():
                           "stock_us": round(t_st, 1)})
             del qd, kd, vd
     sdpa["sweep"] = sweep
+    # Small batches, graph-timed: 20 calls captured in a HIP graph and
+    # replayed, so the figure is device time (eager calls at these sizes are
+    # bound by the host's per-call cost).
+    graph_cells = []
+    for Bd in (1, 2, 4, 8):
+        for Nd in (2048, 8192):
+            qd = torch.randn(Bd, H, 1, D, generator=g).to(torch.bfloat16).to(dev)
+            kd = torch.randn(Bd, Hkv, Nd, D, generator=g).to(torch.bfloat16).to(dev)
+            vd = torch.randn(Bd, Hkv, Nd, D, generator=g).to(torch.bfloat16).to(dev)
+            t_g = graph_us(torch, lambda: bi.scaled_dot_product_attention(qd, kd, vd, scale=sc))
+            by_d = sdpa_bytes(Bd, H, Hkv, Nd, D)
+            graph_cells.append({"B": Bd, "N": Nd, "bi_us": round(t_g, 2),
+                                "gbps": round(by_d / t_g / 1e3, 1),
+                                "hbm_frac": round(by_d / t_g / 1e3 / PEAK_HBM_GBS, 4)})
+            del qd, kd, vd
+    sdpa["graph_timed"] = graph_cells
 
     # Causal prefill attention (the query-row-blocked path of the same kernel):
     # B=1, 32/8 heads, D=128, 2048 query rows over 2048 keys.
@@ -486,6 +632,7 @@ def main():
         for b in (2, 3, 8, 16, 17, 33, 64, 65, 128, 255, 256):
             differing += int((bits(bi.matmul(a[:b].contiguous(), w)[0]) != ref).sum())
 
+    prefill_gemm = prefill_gemms(torch, bi, dev)
     model = None if args.no_model else model_determinism(torch, bi, dev)
     cpu = None if args.no_cpu else cpu_baseline(ops)
 
@@ -501,6 +648,7 @@ def main():
         "per_shape": per_shape,
         "sweep_other_dtypes": other_dtypes,
         "sdpa_decode": sdpa,
+        "prefill_gemm_m4096": prefill_gemm,
         "sdpa_prefill": prefill,
         "quantized_linear": quant,
         "invariance_bits_differing_batch_1_to_256": differing,

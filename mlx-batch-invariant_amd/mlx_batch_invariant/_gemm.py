@@ -144,6 +144,11 @@ def matmul_timed(a, b, start, stop):
     return _gemm_eager(a, b, None, False, events=(start, stop))
 
 
+def linear_timed(x, w, start, stop):
+    """linear(x, w) timed like matmul_timed (the kernel's own timestamps)."""
+    return _gemm_eager(x, w, None, True, events=(start, stop))
+
+
 def matmul(a, b):
     """a @ b with b laid out (K, N). Bitwise independent of a's leading dimensions."""
     return _gemm(a, b, None, transpose_b=False)
