@@ -510,6 +510,8 @@ int sdpa_run(const void* q, const void* k, const void* v, const void* mask,
     return bi::fail(BI_EINVAL, "bi_sdpa: q, k and v must be 16-byte aligned");
   for (int i = 0; i < 3; i++) p.ms[i] = (mask_mode == BI_MASK_ARRAY) ? mask_strides[i] : 0;
   p.scale2 = scale * 1.4426950408889634f;
+  p.ascale2 = (scale < 0.f ? -scale : scale) * 1.4426950408889634f;
+  p.qsign = scale < 0.f ? 0x80008000u : 0u;
   p.mask_mode = mask_mode;
   p.causal_offset = mask_mode == BI_MASK_CAUSAL ? causal_offset : 0;
 

@@ -16,6 +16,12 @@ struct SdpaArgs {
   int64_t B, H, Hkv, qL, N;
   int64_t qs[3], ks[3], vs[3], ms[3];  // element strides for (b, h, s|n)
   float scale2;                        // scale * log2(e)
+  // The matrix-core kernels scale raw scores by |scale| * log2(e) and take a
+  // negative scale as negated queries: qsign (0x80008000 then, else 0) is
+  // XORed into every dword of q as it is loaded, which negates each score
+  // exactly.
+  float ascale2;
+  uint32_t qsign;
   int mask_mode;
   int64_t causal_offset;
 };

@@ -18,22 +18,25 @@
 //     belongs to chain b mod 4; each chain walks its blocks in ascending order.
 //   * Score: raw_i = q . k_i as a chain of v_mfma_f32_16x16x32_{bf16,f16}
 //     over the head dim in ascending 32-element chunks from +0.0 (exact
-//     products, fp32 sums); s_i = raw_i * (scale * log2 e), plus
-//     mask_i * log2 e for an additive mask.
+//     products, fp32 sums). With a = |scale| * log2 e (a negative scale
+//     negates q's elements, which negates every raw_i exactly), the scaled
+//     score is s_i = raw_i * a, plus mask_i * log2 e for an additive mask.
 //   * Key i is used iff i < N, i <= row + causal_offset (causal) and
 //     mask_i > -3e38 (array mask) (reference :92-96).
 //   * Each chain runs an online softmax in base 2 over its blocks: with M the
-//     largest used score of the block (none: the block leaves the chain
-//     unchanged), m' = M > m + 8 ? M : m (a lazily moved base: p <= 2^8),
+//     largest used s_i of the block (without a mask taken as max_i(raw_i) * a,
+//     the same value since rounding is monotonic; none used: the block leaves
+//     the chain unchanged), m' = M > m + 8 ? M : m (a lazily moved base),
 //     f = m' == m ? 1 : exp2(m - m'),
-//     p_i = exp2(s_i - m') (0 for unused keys), l = fma(l, f, sum_i p_i) with
+//     p_i = exp2(fma(raw_i, a, t_i)) with t_i = -m' (array mask:
+//     mask_i * log2 e - m'; 0 for unused keys), l = fma(l, f, sum_i p_i) with
 //     the block sum taken in a fixed tree; o = o * f + 0.0 (skipped when
-//     f == 1, which changes no bits), then o += p . v as two
+//     f == 1, which changes no bits), then o += p . v as one
 //     v_mfma_f32_16x16x32_{bf16,f16} over the block's 32 keys per 16-dim block,
-//     first with p's hi plane, then with its lo plane = T(p - hi), hi = p
-//     truncated to bf16 (bf16) or T(p) (f16); in both, lane group g supplies
+//     p rounded once to T (round to nearest even); lane group g supplies
 //     keys 4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3. m starts at the lowest
-//     finite float and l at 0 (reference :76-79).
+//     finite float and l at 0 (reference :76-79). A mask of zeros gives the
+//     bits of no mask.
 //   * Merge: a sink (reference :80-86, an extra denominator term exp(sink))
 //     enters here as one more partial with m = sink * log2 e, l = 1, o = 0,
 //     ahead of the chains: M = max of the sink's and the chains' m;
@@ -41,7 +44,7 @@
 //     c = 0, 1, 2, 3 in order, e_c = exp2(m_c - M), L = fma(l_c, e_c, L) and
 //     O = fma(o_c, e_c, O); out = L == 0 ? O : O / L, one rounding to T.
 //     (Seeding a chain's base with the sink, as the reference seeds its
-//     simdgroup 0, would put a large sink's p below the f16 planes' range.)
+//     simdgroup 0, would put a large sink's p below f16's range.)
 // Every column, whatever workgroup or lane it lands in, however many rows or
 // heads share its keys and whatever the launch shape (columns per workgroup,
 // prefetch depths), runs exactly this sequence: an output row has the same
@@ -151,35 +154,27 @@ template <typename T> __device__ inline unsigned short tbits(T x) {
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-// Splits four probabilities p (finite, >= 0) into two 16-bit planes packed
-// two per dword, element e in bits 16 (e % 2) of dword e / 2: hi + lo = p to
-// about 16 significant bits. bf16: hi is p's upper 16 bits (p truncated, so
-// p - hi is exact) and lo = RNE(p - hi). f16: hi = RNE(p), lo = RNE(p - hi).
+// Four probabilities p (finite, >= 0) rounded to the element type (RNE),
+// packed two per dword: element e in bits 16 (e % 2) of dword e / 2.
 template <typename T>
-__device__ __forceinline__ void split_p(const float (&pv)[4], uint2& ph, uint2& pl) {
-  if constexpr (__is_same(T, __bf16)) {
-    uint32_t h[2], lo[2];
+__device__ __forceinline__ uint2 pack_p(const float (&pv)[4]) {
+  uint32_t w[2];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const uint32_t b0 = __float_as_uint(pv[2 * j]), b1 = __float_as_uint(pv[2 * j + 1]);
-      h[j] = __builtin_amdgcn_perm(b1, b0, 0x07060302);
-      const f32x2_t d = {pv[2 * j] - __uint_as_float(b0 & 0xFFFF0000u),
-                         pv[2 * j + 1] - __uint_as_float(b1 & 0xFFFF0000u)};
-      lo[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(d, bf16x2_t));
+  for (int j = 0; j < 2; j++) {
+    if constexpr (__is_same(T, __bf16)) {
+      const f32x2_t d = {pv[2 * j], pv[2 * j + 1]};
+      w[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(d, bf16x2_t));
+    } else {
+      w[j] = (uint32_t)tbits((T)pv[2 * j]) | ((uint32_t)tbits((T)pv[2 * j + 1]) << 16);
     }
-    ph = make_uint2(h[0], h[1]);
-    pl = make_uint2(lo[0], lo[1]);
-  } else {
-    unsigned short hb[4], lb[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const T hi = (T)pv[e];
-      hb[e] = tbits(hi);
-      lb[e] = tbits((T)(pv[e] - (float)hi));
-    }
-    ph = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
-    pl = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
   }
+  return make_uint2(w[0], w[1]);
+}
+
+// A query chunk with every element's sign flipped when qsign is 0x80008000
+// (a negative scale), unchanged when it is 0.
+__device__ __forceinline__ uint4 qneg(uint4 q, uint32_t qsign) {
+  return make_uint4(q.x ^ qsign, q.y ^ qsign, q.z ^ qsign, q.w ^ qsign);
 }
 
 __device__ inline int xcd_remap(int w, int total) {
@@ -470,7 +465,7 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
     const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + head[ct] * p.qs[1] + srow[ct] * p.qs[2];
 #pragma unroll
     for (int i = 0; i < NQ; i++)
-      qt[ct][i] = colv[ct] ? ld16(qrow + 32 * i + 8 * g) : make_uint4(0, 0, 0, 0);
+      qt[ct][i] = colv[ct] ? qneg(ld16(qrow + 32 * i + 8 * g), p.qsign) : make_uint4(0, 0, 0, 0);
     mrow[ct] = head[ct] * p.ms[1] + srow[ct] * p.ms[2];
     m[ct] = -FLT_MAX;
     l[ct] = 0.f;
@@ -599,7 +594,7 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
     static_assert(!VPRE || C::ASM_TR, "values read ahead by asm reads only");
     // Key indices fit in 32 bits (the host checks N < 2^31).
     const int key0 = (int)blk * kBlk + 4 * g;
-    uint2 ph[CT][2], pl[CT][2];
+    uint2 ph[CT][2];
     float f[CT];
     uint32_t used = 0;  // mask: bit 4kt + e set if this lane's column uses key 16kt + 4g + e
     // FULL: every column of the workgroup uses all 32 keys of the block (no
@@ -609,15 +604,18 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
       constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
       for (int ct = 0; ct < CT; ct++) {
-        float s[2][4];
+        // Raw scores r (q . k) and the exponent's addend t: p = exp2(fma(r,
+        // a, t)) with a = |scale| * log2 e, t = -m' (or mask * log2 e - m').
+        float r[2][4], t[2][4];
         bool use[2][4];
 #pragma unroll
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            s[kt][e] = sc[ct][kt][e] * p.scale2;
+            r[kt][e] = sc[ct][kt][e];
             use[kt][e] = FULL || key0 + 16 * kt + e < kend[ct];
           }
+        float bm = -INFINITY;
         if constexpr (MK) {  // keys past N read 0 and are unused
 #pragma unroll
           for (int kt = 0; kt < 2; kt++)
@@ -625,18 +623,21 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
             for (int e = 0; e < 4; e++) {
               const float mv = (float)__builtin_bit_cast(T, mk[ct][4 * kt + e]);
               use[kt][e] = use[kt][e] && mv > -3.0e38f;
-              s[kt][e] = s[kt][e] + mv * kLog2e;
+              t[kt][e] = mv * kLog2e;
+              const float sv = r[kt][e] * p.ascale2 + t[kt][e];
+              bm = use[kt][e] ? fmaxf(bm, sv) : bm;
+              used |= use[kt][e] ? 1u << (4 * kt + e) : 0u;
             }
+          bm = col_max(bm);
+        } else {
+          // Rounding is monotonic: the largest raw score, scaled, is the
+          // largest scaled score.
+#pragma unroll
+          for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) bm = use[kt][e] ? fmaxf(bm, r[kt][e]) : bm;
+          bm = col_max(bm) * p.ascale2;
         }
-        float bm = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
-            if constexpr (MK != 0) used |= use[kt][e] ? 1u << (4 * kt + e) : 0u;
-          }
-        bm = col_max(bm);
         const bool any = bm > -INFINITY;
         // The base moves only when the block's largest score passes it by more
         // than 8 (p then stays <= 2^8): few rescales, the same result after o / l.
@@ -648,15 +649,16 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(s[kt][e] - mn) : 0.f;
+            const float tt = MK ? t[kt][e] - mn : -mn;
+            pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(__builtin_fmaf(r[kt][e], p.ascale2, tt)) : 0.f;
             ps = ps + pv[kt][e];
           }
         ps = col_sum(ps);
         l[ct] = __builtin_fmaf(l[ct], f[ct], ps);
         m[ct] = mn;
-        // P^T as the B operand of the 16x16x16 MFMAs, split into two planes.
+        // P^T as the B operand of the P.V MFMAs, rounded once to T.
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++) split_p<T>(pv[kt], ph[ct][kt], pl[ct][kt]);
+        for (int kt = 0; kt < 2; kt++) ph[ct][kt] = pack_p<T>(pv[kt]);
       }
     };
     if (!MK && (blk + 1) * kBlk <= kfull)
@@ -721,7 +723,6 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
 #pragma unroll
       for (int ct = 0; ct < CT; ct++) {
         o[ct][db] = mma32(T(0), vt, join(ph[ct][0], ph[ct][1]), o[ct][db]);
-        o[ct][db] = mma32(T(0), vt, join(pl[ct][0], pl[ct][1]), o[ct][db]);
       }
     }
   };
@@ -1028,7 +1029,8 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
   {
     const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + head * p.qs[1] + srow * p.qs[2];
 #pragma unroll
-    for (int i = 0; i < NQ; i++) qt[i] = colv ? ld16(qrow + 32 * i + 8 * g) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < NQ; i++)
+      qt[i] = colv ? qneg(ld16(qrow + 32 * i + 8 * g), p.qsign) : make_uint4(0, 0, 0, 0);
   }
   float m[4], l[4];
   f32x4_t o[4][NB];
@@ -1123,25 +1125,20 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
     // Softmax of chain c over the block (the per-column steps of
     // sdpa_mfma_kernel, in the same order).
     const int key0 = (int)blk * kBlk + 4 * g;
-    uint2 ph[2], pl[2];
+    uint2 ph[2];
     float f;
     auto softmax = [&](auto full_tag) __attribute__((always_inline)) {
       constexpr bool FULL = decltype(full_tag)::value;
-      float s[2][4];
       bool use[2][4];
-#pragma unroll
-      for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          s[kt][e] = sc[kt][e] * p.scale2;
-          use[kt][e] = FULL || key0 + 16 * kt + e < kend;
-        }
       float bm = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) bm = use[kt][e] ? fmaxf(bm, s[kt][e]) : bm;
-      bm = col_max(bm);
+        for (int e = 0; e < 4; e++) {
+          use[kt][e] = FULL || key0 + 16 * kt + e < kend;
+          bm = use[kt][e] ? fmaxf(bm, sc[kt][e]) : bm;
+        }
+      bm = col_max(bm) * p.ascale2;
       const bool any = bm > -INFINITY;
       const float mn = (any && bm > m[c] + 8.f) ? bm : m[c];
       f = mn == m[c] ? 1.f : __builtin_amdgcn_exp2f(m[c] - mn);
@@ -1151,14 +1148,14 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
       for (int kt = 0; kt < 2; kt++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(s[kt][e] - mn) : 0.f;
+          pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][e], p.ascale2, -mn)) : 0.f;
           ps = ps + pv[kt][e];
         }
       ps = col_sum(ps);
       l[c] = __builtin_fmaf(l[c], f, ps);
       m[c] = mn;
 #pragma unroll
-      for (int kt = 0; kt < 2; kt++) split_p<T>(pv[kt], ph[kt], pl[kt]);
+      for (int kt = 0; kt < 2; kt++) ph[kt] = pack_p<T>(pv[kt]);
     };
     if ((blk + 1) * kBlk <= kfull_w)
       softmax(std::true_type{});
@@ -1172,13 +1169,12 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
     for (int db = 0; db < NB; db++) asm volatile("" : "+v"(va[db][0]), "+v"(va[db][1]));
-    // o += P . V over the block's 32 keys, hi plane then lo plane.
+    // o += P . V over the block's 32 keys.
 #pragma unroll
     for (int db = 0; db < NB; db++) {
       const uint4 vt =
           join(__builtin_bit_cast(uint2, va[db][0]), __builtin_bit_cast(uint2, va[db][1]));
       o[c][db] = mma32(T(0), vt, join(ph[0], ph[1]), o[c][db]);
-      o[c][db] = mma32(T(0), vt, join(pl[0], pl[1]), o[c][db]);
     }
   };
 
