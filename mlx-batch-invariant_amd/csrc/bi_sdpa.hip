@@ -389,8 +389,12 @@ SdpaKernelFn mfma_kernel(int64_t D, int64_t V, int dtype, bool mask, int shape) 
 // chunks of prefill such as 16 query rows.
 int mfma_pick_shape(int64_t D, int64_t V, int64_t ncol, int64_t streams, bool array_mask,
                     int cus) {
-  if (ncol > 16 && D == 128 && V == 128 && !array_mask) {
-    const int sc = sdpa_shape_columns(D, V, SDPA_SHARED);
+  // Shared needs its workgroups at least half full: with a few query rows
+  // per kv head (B = 64, qL = 5 or 8: 20 or 32 of 128 columns) most of its
+  // waves would idle while the others walk every block (rows 360 us against
+  // 387 us at N = 8192); from 64 columns it leads (qL = 17: 416 against 579 us).
+  const int sc = sdpa_shape_columns(D, V, SDPA_SHARED);
+  if (2 * ncol >= sc && D == 128 && V == 128 && !array_mask) {
     const int64_t w = streams * ((ncol + sc - 1) / sc);
     const int64_t rounds = (w + cus - 1) / cus;
     if (w >= 2 * (int64_t)cus || (5 * w >= 4 * (int64_t)cus && 4 * w >= 3 * rounds * cus))

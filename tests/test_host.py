@@ -200,6 +200,10 @@ def test_sdpa_shape_policy():
     assert pick(1, 896) == pick(1, 1024) == pick(1, 1536) == _lib.SDPA_SHARED  # 224, 256, 384
     assert pick(1, 2048) == pick(4, 1024) == _lib.SDPA_SHARED  # D = V = 128, no array mask
     assert pick(1, 2048, mask=_lib.MASK_CAUSAL) == _lib.SDPA_SHARED
+    # Multi-token decode at large batch: shared only from 64 columns per kv
+    # head (half of its 128), rows below.
+    assert pick(64, 5) == pick(64, 8) == pick(32, 8) == _lib.SDPA_ROWS
+    assert pick(64, 17) == pick(32, 17) == _lib.SDPA_SHARED
     assert pick(1, 2048, mask=_lib.MASK_ARRAY) == _lib.SDPA_ROWS
     assert pick(1, 2048, D=64, V=64) == _lib.SDPA_ROWS
     assert pick(1, 2048, D=256, V=256) == _lib.SDPA_ROWS
