@@ -111,8 +111,11 @@ int bi_gemm(const void* a, const void* b, const void* bias, void* out,
  * key that is visible to another query row of the same 32-key block, but not
  * to this one, by zero; a NaN or infinity there, which reaches that other
  * row's output in any case, also reaches this row's.
- * Supported head dims (D, V): D == V in {32, 64, 96, 128, 160, 192, 224, 256}
- * and (192, 128); other multiples of 32 return BI_EUNSUPPORTED.
+ * Supported head dims (D, V): D == V in {32, 64, 96, ..., 512} (every multiple
+ * of 32 up to 512) and (192, 128), (128, 64), (64, 128), (256, 128), (128, 256),
+ * (576, 512); other multiples of 32 return BI_EUNSUPPORTED (each pair is a
+ * compiled kernel set). fp32 heads above 352 keep part of their state in
+ * scratch memory (correct, slower).
  */
 int bi_sdpa(const void* q, const void* k, const void* v,
             const void* mask, const int64_t* mask_strides,

@@ -473,7 +473,8 @@ int sdpa_run(const void* q, const void* k, const void* v, const void* mask,
     return bi::fail(BI_EINVAL, "bi_sdpa: array mask needs a mask pointer and strides");
   if (!dims_built(D, V))
     return bi::fail(BI_EUNSUPPORTED, "bi_sdpa: head dims D=%lld V=%lld are not built "
-                    "(supported: D == V in {32, 64, ..., 256}, and D = 192 with V = 128)",
+                    "(supported: D == V in {32, 64, ..., 512}; (D, V) in {(192, 128), (128, 64), "
+                    "(64, 128), (256, 128), (128, 256), (576, 512)})",
                     (long long)D, (long long)V);
   const int64_t rows = B * H * qL;
   if (rows == 0) return BI_OK;

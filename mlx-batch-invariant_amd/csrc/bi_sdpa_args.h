@@ -31,9 +31,10 @@ typedef void (*SdpaKernelFn)(SdpaArgs);
 // Head-dim pairs (D for queries and keys, V for values) built for every
 // element type. The reference accepts any multiples of 32
 // (mlx_batch_invariant/_attention.py:224-227); these are the ones compiled.
-#define BI_SDPA_DIM_PAIRS(X) \
-  X(32, 32) X(64, 64) X(96, 96) X(128, 128) X(160, 160) X(192, 192) X(224, 224) X(256, 256) \
-  X(192, 128)
+#define BI_SDPA_DIM_PAIRS(X)                                                                   \
+  X(32, 32) X(64, 64) X(96, 96) X(128, 128) X(160, 160) X(192, 192) X(224, 224) X(256, 256)     \
+  X(288, 288) X(320, 320) X(352, 352) X(384, 384) X(416, 416) X(448, 448) X(480, 480)          \
+  X(512, 512) X(192, 128) X(128, 64) X(64, 128) X(256, 128) X(128, 256) X(576, 512)
 
 // Launch shapes of the MFMA kernel (bf16 / f16). None of them enters a
 // column's arithmetic; they decide which workgroup, wave and lane evaluate a
@@ -47,7 +48,7 @@ typedef void (*SdpaKernelFn)(SdpaArgs);
 //   SDPA_SHARED  one 16-column tile per wave, every wave walking every key
 //                block with all 4 chains' state of its columns: a key and value
 //                block is loaded once into LDS for 4-8 column tiles (prefill;
-//                D and V in {32, 64, 128})
+//                D = V in {32, 64, 128})
 enum SdpaShape { SDPA_ROWS = 0, SDPA_TILE = 1, SDPA_SPLIT2 = 2, SDPA_SPLIT4 = 3, SDPA_SPLIT8 = 4,
                  SDPA_SHARED = 5, SDPA_NUM_SHAPES = 6 };
 
@@ -59,10 +60,10 @@ constexpr int sdpa_splits_max(int64_t V) {
   return (V / 16) % 8 == 0 ? 8 : (V / 16) % 4 == 0 ? 4 : (V / 16) % 2 == 0 ? 2 : 1;
 }
 constexpr int sdpa_splits_min(int64_t V) { return V > 128 ? 2 : 1; }
-// SDPA_SHARED: built for D and V in {32, 64, 128}; its waves split the
+// SDPA_SHARED: built for D = V in {32, 64, 128}; its waves split the
 // (D + V) / 16 loads of a key block evenly, at most 8 waves.
 constexpr bool sdpa_shared_dims(int64_t D, int64_t V) {
-  return (D == 32 || D == 64 || D == 128) && (V == 32 || V == 64 || V == 128);
+  return D == V && (D == 32 || D == 64 || D == 128);
 }
 constexpr int sdpa_shared_waves(int64_t D, int64_t V) {
   return (D + V) / 16 >= 8 ? 8 : (int)((D + V) / 16);

@@ -24,8 +24,8 @@ PARTIALS = 32     # partial softmaxes per row = stride over the key sequence
 GROUP_LANES = 8   # lanes that share one key's dot product
 # Built (D, V) head-dim pairs: D for queries and keys, V for values
 # (csrc/bi_sdpa_args.h BI_SDPA_DIM_PAIRS).
-HEAD_DIMS = ((32, 32), (64, 64), (96, 96), (128, 128), (160, 160), (192, 192), (224, 224),
-             (256, 256), (192, 128))
+HEAD_DIMS = tuple((d, d) for d in range(32, 513, 32)) + (
+    (192, 128), (128, 64), (64, 128), (256, 128), (128, 256), (576, 512))
 HEAD_DIM_MULTIPLE = 32      # the reference's own requirement (_attention.py:224-227)
 
 _SUPPORTED = (torch.float32, torch.float16, torch.bfloat16)

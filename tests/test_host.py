@@ -122,8 +122,8 @@ def test_sdpa_abi_rejects_bad_arguments_without_a_gpu():
 
     assert call(H=6, Hkv=4) == _lib.EINVAL and "multiple" in _err()
     assert call(D=48, V=48) == _lib.EUNSUPPORTED and "head dims" in _err()
-    assert call(D=128, V=64) == _lib.EUNSUPPORTED
-    assert call(D=288, V=288) == _lib.EUNSUPPORTED
+    assert call(D=128, V=96) == _lib.EUNSUPPORTED
+    assert call(D=544, V=544) == _lib.EUNSUPPORTED
     assert call(mode=5) == _lib.EINVAL
     assert call(mode=2) == _lib.EINVAL and "mask" in _err()
     assert call(dtype=9) == _lib.EINVAL
@@ -146,6 +146,7 @@ def test_sdpa_shape_abi_without_a_gpu():
     assert forced(3, dtype=_lib.F32) == _lib.EINVAL      # 8 heads per workgroup: D <= 64 only
     assert forced(2, dtype=_lib.F32, H=8, Hkv=4) == _lib.EINVAL  # 4 heads do not divide 2
     assert forced(0, D=96, V=64) == _lib.EUNSUPPORTED
+    assert forced(0, D=544, V=544) == _lib.EUNSUPPORTED
 
     def info(D, V, shape, dtype=_lib.BF16):
         c, w = ctypes.c_int(), ctypes.c_int()
@@ -170,6 +171,10 @@ def test_sdpa_shape_abi_without_a_gpu():
     assert info(64, 64, 3, _lib.F32) == (8, 1)
     assert info(128, 128, 3, _lib.F32) == _lib.EINVAL
     assert info(256, 256, 1, _lib.F32) == (2, 1)
+    assert info(128, 64, _lib.SDPA_ROWS) == (32, 1) and info(64, 128, _lib.SDPA_SPLIT8) == (16, 8)
+    assert info(576, 512, _lib.SDPA_ROWS) == (16, 2)     # latent-attention heads: one tile
+    assert info(64, 128, _lib.SDPA_SHARED) == _lib.EINVAL  # shared: D = V only
+    assert info(512, 512, _lib.SDPA_SPLIT8) == (16, 8)
 
 
 def test_sdpa_shape_policy():
@@ -237,8 +242,8 @@ def test_tile_contract_is_pinned():
     assert {"BM", "BN", "BK", "SG_M", "SG_N"} <= set(bi.TILE)
     assert bi.TILE["BK"] == bi.TILE["K_CHUNK_16BIT"]
     assert _attention.PARTIALS == 32 and _attention.GROUP_LANES == 8
-    assert bi.HEAD_DIMS == ((32, 32), (64, 64), (96, 96), (128, 128), (160, 160), (192, 192),
-                            (224, 224), (256, 256), (192, 128))
+    assert bi.HEAD_DIMS == tuple((d, d) for d in range(32, 513, 32)) + (
+        (192, 128), (128, 64), (64, 128), (256, 128), (128, 256), (576, 512))
 
 
 # ------------------------------------------------------------ Python validation
@@ -280,8 +285,8 @@ def test_sdpa_validation_matches_reference():
         bi.scaled_dot_product_attention(_t(1, 4, 1, 48), _t(1, 4, 8, 48), _t(1, 4, 8, 48))
     with pytest.raises(NotImplementedError, match="not built"):  # D != V pairs not compiled
         bi.scaled_dot_product_attention(_t(1, 4, 1, 96), _t(1, 4, 8, 96), _t(1, 4, 8, 64))
-    with pytest.raises(NotImplementedError, match="not built"):  # above 256
-        bi.scaled_dot_product_attention(_t(1, 4, 1, 288), _t(1, 4, 8, 288), _t(1, 4, 8, 288))
+    with pytest.raises(NotImplementedError, match="not built"):  # above 512
+        bi.scaled_dot_product_attention(_t(1, 4, 1, 544), _t(1, 4, 8, 544), _t(1, 4, 8, 544))
     with pytest.raises(ValueError, match="sinks"):  # reference tests:355-364
         bi.scaled_dot_product_attention(q, k, v, sinks=torch.zeros(4))
     with pytest.raises(ValueError, match="causal"):
