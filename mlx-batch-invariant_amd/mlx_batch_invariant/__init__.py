@@ -112,8 +112,10 @@ class _Patches:
 
 @contextlib.contextmanager
 def batch_invariant_mode(strict=True):
-    """Route torch.matmul, torch.addmm, ``@``, nn.Linear / F.linear and
-    F.scaled_dot_product_attention through the invariant kernels.
+    """Route torch.matmul, torch.mm, torch.addmm, ``@``, nn.Linear / F.linear
+    and F.scaled_dot_product_attention through the invariant kernels
+    (torch.bmm and torch.einsum are not routed: they stay stock and
+    batch-variant).
 
     Calls the kernels cannot make invariant raise ``NotImplementedError``. With
     ``strict=False`` they fall back to stock PyTorch instead, which means the
@@ -138,6 +140,8 @@ def batch_invariant_mode(strict=True):
         "addmm": torch.addmm,
         "tensor_matmul_op": torch.Tensor.__matmul__,
         "tensor_matmul": torch.Tensor.matmul,
+        "mm": torch.mm,
+        "tensor_mm": torch.Tensor.mm,
         "linear_forward": torch.nn.Linear.forward,
         "F_linear": F.linear,
         "sdpa": F.scaled_dot_product_attention,
@@ -148,6 +152,14 @@ def batch_invariant_mode(strict=True):
             return _unsupported(
                 "matmul with shapes %s @ %s" % (_shape(a), _shape(b)),
                 strict, saved["matmul"], a, b, *args, **kwargs)
+        return matmul(a, b)
+
+    def bi_mm(a, b, *args, **kwargs):
+        # torch.mm takes two 2-D matrices; the same kernel as matmul.
+        if (args or kwargs or not _kernel_ready(a, b) or a.ndim != 2 or b.ndim != 2):
+            return _unsupported(
+                "mm with shapes %s @ %s" % (_shape(a), _shape(b)),
+                strict, saved["mm"], a, b, *args, **kwargs)
         return matmul(a, b)
 
     def bi_addmm(c, a, b, *args, beta=1, alpha=1, **kwargs):
@@ -213,6 +225,8 @@ def batch_invariant_mode(strict=True):
     patches.set(torch, "addmm", bi_addmm)
     patches.set(torch.Tensor, "__matmul__", lambda a, b: bi_matmul(a, b))
     patches.set(torch.Tensor, "matmul", lambda a, b: bi_matmul(a, b))
+    patches.set(torch, "mm", bi_mm)
+    patches.set(torch.Tensor, "mm", lambda a, b: bi_mm(a, b))
     patches.set(torch.nn.Linear, "forward", bi_linear_forward)
     patches.set(F, "linear", bi_linear)
     patches.set(F, "scaled_dot_product_attention", bi_sdpa)

@@ -34,9 +34,11 @@ def test_routed_calls_match_direct_kernels(cuda):
                           lin=lin(a),
                           sdpa=F.scaled_dot_product_attention(q, k, v, scale=0.3, enable_gqa=True))
             op = a @ w
+            mm_fn, mm_method = torch.mm(a, w), a.mm(w)
     for key in direct:
         assert ndiff(direct[key], routed[key]) == 0, key
     assert ndiff(op, direct["mm"]) == 0
+    assert ndiff(mm_fn, direct["mm"]) == 0 and ndiff(mm_method, direct["mm"]) == 0
 
 
 def test_is_causal_is_aligned_to_the_start(cuda):

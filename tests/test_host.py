@@ -353,6 +353,8 @@ def test_shim_routes_supported_calls(stubbed):
         assert torch.matmul(a, w).routed_to == "bi:matmul"
         assert (a @ w).routed_to == "bi:matmul"
         assert a.matmul(w).routed_to == "bi:matmul"
+        assert torch.mm(a, w).routed_to == "bi:matmul"
+        assert a.mm(w).routed_to == "bi:matmul"
         assert torch.addmm(c, a, w).routed_to == "bi:addmm"
         lin = torch.nn.Linear(8, 5)
         assert lin(a).routed_to == "bi:linear"
@@ -365,7 +367,7 @@ def test_shim_routes_supported_calls(stubbed):
         y = F.scaled_dot_product_attention(q, k, k, is_causal=True, enable_gqa=True)
         assert y.routed_to == "bi:sdpa"
     assert not bi.is_enabled()
-    assert stubbed.calls.count("matmul") == 3 and "addmm" in stubbed.calls
+    assert stubbed.calls.count("matmul") == 5 and "addmm" in stubbed.calls
 
 
 def test_strict_raises_and_non_strict_falls_back(stubbed):
@@ -381,6 +383,8 @@ def test_strict_raises_and_non_strict_falls_back(stubbed):
         with pytest.raises(NotImplementedError):
             torch.addmm(torch.randn(3, 5), torch.randn(3, 8), torch.randn(8, 5))  # 2-D input
         with pytest.raises(NotImplementedError):
+            torch.mm(torch.randn(2, 3, 8), torch.randn(8, 5))  # mm takes 2-D operands only
+        with pytest.raises(NotImplementedError):
             F.scaled_dot_product_attention(torch.randn(1, 4, 2, 64), torch.randn(1, 4, 8, 64),
                                            torch.randn(1, 4, 8, 64), dropout_p=0.1)
         g = torch.randn(3, 8, requires_grad=True)
@@ -394,14 +398,16 @@ def test_strict_raises_and_non_strict_falls_back(stubbed):
 def test_originals_restored_even_on_exception():
     """Reference tests:686-698."""
     before = (torch.matmul, torch.addmm, torch.Tensor.__matmul__, torch.Tensor.matmul,
-              torch.nn.Linear.forward, F.linear, F.scaled_dot_product_attention)
-    had = {n: n in vars(torch.Tensor) for n in ("__matmul__", "matmul")}
+              torch.mm, torch.Tensor.mm, torch.nn.Linear.forward, F.linear,
+              F.scaled_dot_product_attention)
+    had = {n: n in vars(torch.Tensor) for n in ("__matmul__", "matmul", "mm")}
     with pytest.raises(RuntimeError):
         with bi.batch_invariant_mode():
             assert bi.is_enabled()
             raise RuntimeError("boom")
     after = (torch.matmul, torch.addmm, torch.Tensor.__matmul__, torch.Tensor.matmul,
-             torch.nn.Linear.forward, F.linear, F.scaled_dot_product_attention)
+             torch.mm, torch.Tensor.mm, torch.nn.Linear.forward, F.linear,
+             F.scaled_dot_product_attention)
     assert before == after
     assert {n: n in vars(torch.Tensor) for n in had} == had
     assert not bi.is_enabled()
