@@ -200,15 +200,20 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t byt
 // one per 16-lane row). permlane16_swap pairs rows (0, 1) and (2, 3),
 // permlane32_swap the two halves; every lane adds its pair's operands in the
 // same order (lower row first), so all four end with identical bits.
+// The larger of two lanes' block maxima as a compare and select (fmaxf
+// would first canonicalise both operands: two more instructions). The maxima
+// are never NaN (fmaxf skips NaN scores), and which of +0 / -0 it keeps
+// changes no probability's bits.
+__device__ __forceinline__ float smax(float a, float b) { return a > b ? a : b; }
 __device__ inline float row_pair(float x, bool is_max) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
-  return is_max ? fmaxf(a, b) : a + b;
+  return is_max ? smax(a, b) : a + b;
 }
 __device__ inline float half_pair(float x, bool is_max) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
-  return is_max ? fmaxf(a, b) : a + b;
+  return is_max ? smax(a, b) : a + b;
 }
 __device__ inline float col_sum(float x) { return half_pair(row_pair(x, false), false); }
 __device__ inline float col_max(float x) { return half_pair(row_pair(x, true), true); }
@@ -651,7 +656,7 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
           for (int e = 0; e < 4; e++) {
             const float tt = MK ? t[kt][e] - mn : -mn;
             pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(__builtin_fmaf(r[kt][e], p.ascale2, tt)) : 0.f;
-            ps = ps + pv[kt][e];
+            ps = kt + e == 0 ? pv[0][0] : ps + pv[kt][e];  // p >= +0: the same as 0 + p
           }
         ps = col_sum(ps);
         l[ct] = __builtin_fmaf(l[ct], f[ct], ps);
@@ -1149,7 +1154,7 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           pv[kt][e] = use[kt][e] ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][e], p.ascale2, -mn)) : 0.f;
-          ps = ps + pv[kt][e];
+          ps = kt + e == 0 ? pv[0][0] : ps + pv[kt][e];  // p >= +0: the same as 0 + p
         }
       ps = col_sum(ps);
       l[c] = __builtin_fmaf(l[c], f, ps);
