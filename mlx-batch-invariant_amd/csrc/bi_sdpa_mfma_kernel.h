@@ -893,7 +893,7 @@ __device__ __forceinline__ void static_for(F& f) {
 // wave has finished group g - 1, whose slots then take group g + 1's loads.
 // Between barriers the waves drift apart, so one wave's softmax overlaps
 // another's products on the same SIMD.
-template <typename T, int D, int V, int NW, int GP>
+template <typename T, int D, int V, int NW, int GP, int NG>
 struct Shared {
   static constexpr int NQ = D / 32;        // score MFMAs per 16 keys
   static constexpr int NB = V / 16;        // 16-dim blocks of o
@@ -903,16 +903,18 @@ struct Shared {
   static constexpr int SLOT = KSLOT + kBlk * VCH;  // uint4 per slot (keys, then values)
   static constexpr int NL = SLOT / 64;     // LDS-DMA loads per block
   static constexpr int LPW = NL / NW;      // of them issued by each wave
-  static constexpr int S = 2 * GP;         // slots
+  static constexpr int S = NG * GP;        // slots
   static constexpr int HALF = GP * SLOT * 16;  // bytes of one group's slots
-  // Whether the two groups need their own lane address registers (LDS read
-  // offsets are 16-bit immediates).
-  static constexpr bool TWO_BASES = 2 * HALF > 65536;
+  // Lane address registers: one per 64 KB of slots (LDS read offsets are
+  // 16-bit immediates; a slot starts at most 48 KB into its window and its
+  // reads stay within 16 KB of that).
+  static constexpr int NBASE = (S * SLOT * 16 + 65535) / 65536;
   static_assert(NL % NW == 0 && (CH & (CH - 1)) == 0 && (VCH & (VCH - 1)) == 0 && D <= 128 &&
                     V <= 128 && VCH >= 4 && (4 % GP == 0 || GP % 4 == 0),
                 "shape");
-  static_assert(GP * LPW <= 63, "loads in flight exceed the vmcnt range");
-  static_assert(S * SLOT * 16 <= 160 * 1024 && HALF <= 65536, "LDS per workgroup");
+  static_assert(NG >= 2 && (NG - 1) * GP * LPW <= 63, "loads in flight exceed the vmcnt range");
+  static_assert(S * SLOT * 16 <= 160 * 1024 && HALF <= 65536 && SLOT * 16 <= 16384,
+                "LDS per workgroup");
   // Key rows: chunk c of key r at c ^ (r mod CH), so that the 16 keys of a
   // score operand read distinct banks. Value rows: 32-byte pair j of key r at
   // pair (j + rot(r)) mod NPR, rot(r) = (r mod 8) >> (3 - t) with 2^t the
@@ -982,9 +984,9 @@ struct Shared {
   };
 };
 
-template <typename T, int D, int V, int NW, int GP>
+template <typename T, int D, int V, int NW, int GP, int NG>
 __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
-  using C = Shared<T, D, V, NW, GP>;
+  using C = Shared<T, D, V, NW, GP, NG>;
   constexpr int NQ = C::NQ, NB = C::NB, CH = C::CH, VCH = C::VCH, LPW = C::LPW;
   constexpr int COLS = 16 * NW;  // columns per workgroup
   __shared__ uint4 ring[C::S * C::SLOT];
@@ -1049,7 +1051,7 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
 
   typename C::Loads ld;
   ld.init(p, b, kvh, kmax, nblk, wave, lane);
-  // Block i of group half h (0 or 1) into slot h * GP + i mod GP.
+  // Block i of group h (0 .. NG - 1) into slot h * GP + i mod GP.
   auto issue = [&](int64_t i, int slot) __attribute__((always_inline)) {
     ld.issue(i, ring + slot * C::SLOT + wave * LPW * 64);
   };
@@ -1061,7 +1063,7 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
   // + 16: + 16 rows). Slots within a group and key halves are constant
   // offsets. The empty asm keeps each an opaque register, so the unrolled
   // reads do not each recompute theirs.
-  constexpr int NBASE = C::TWO_BASES ? 2 : 1;
+  constexpr int NBASE = C::NBASE;
   uint32_t kofs[NBASE][NQ], vofs[NBASE][NB];
   {
     const uint32_t rb = (uint32_t)(uintptr_t)(lds_void_t*)ring;
@@ -1070,13 +1072,13 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
     for (int h = 0; h < NBASE; h++) {
 #pragma unroll
       for (int i = 0; i < NQ; i++) {
-        kofs[h][i] = rb + h * C::HALF + (r16 * CH + ((4 * i + g) ^ C::swz_k(r16))) * 16;
+        kofs[h][i] = rb + h * 65536 + (r16 * CH + ((4 * i + g) ^ C::swz_k(r16))) * 16;
         asm volatile("" : "+v"(kofs[h][i]));
       }
 #pragma unroll
       for (int db = 0; db < NB; db++) {
         const int col = 16 * db + 4 * (r16 & 3);
-        vofs[h][db] = rb + h * C::HALF + C::KSLOT * 16 +
+        vofs[h][db] = rb + h * 65536 + C::KSLOT * 16 +
                       (kr * VCH + C::vchunk_lds(kr, col >> 3)) * 16 + (col & 7) * 2;
         asm volatile("" : "+v"(vofs[h][db]));
       }
@@ -1088,8 +1090,8 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
   auto compute = [&](auto slot_c, auto chain, int64_t blk) __attribute__((always_inline)) {
     constexpr int c = decltype(chain)::value;
     constexpr int slot = decltype(slot_c)::value;
-    constexpr int h = C::TWO_BASES ? slot / GP : 0;
-    constexpr int SOFF = (slot - h * GP) * C::SLOT * 16;
+    constexpr int h = slot * C::SLOT * 16 / 65536;
+    constexpr int SOFF = slot * C::SLOT * 16 % 65536;
     // Scores: S^T tiles (16 keys x 16 columns); lane (g, r16) holds keys
     // 16kt + 4g + e of column r16.
     // Both key halves' reads are issued first; the first half's products run
@@ -1183,31 +1185,32 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
     }
   };
 
-  // Group q holds blocks q * GP .. + GP - 1 in slots (q mod 2) * GP ..;
-  // group q + 1 loads while group q is computed. A wave skips a block none
-  // of its columns can see (for them it changes nothing). Unrolled over UG
-  // groups (UG * GP a multiple of 4, UG even), so slot and chain indices are
-  // compile-time.
-  constexpr int UG = GP >= 4 ? 2 : 4 / GP;
+  // Group q holds blocks q * GP .. + GP - 1 in slots (q mod NG) * GP ..;
+  // groups q + 1 .. q + NG - 1 load while group q is computed. A wave skips
+  // a block none of its columns can see (for them it changes nothing).
+  // Unrolled over UG groups (UG * GP a multiple of 4, UG a multiple of NG),
+  // so slot and chain indices are compile-time.
+  constexpr int UG = lcm(NG, GP >= 4 ? 1 : 4 / GP);
 #pragma unroll
-  for (int u = 0; u < GP; u++) issue(u, u);
+  for (int u = 0; u < (NG - 1) * GP; u++) issue(u, u);
   int64_t q0 = 0;
   auto group = [&](auto qc) __attribute__((always_inline)) -> bool {
     constexpr int uq = decltype(qc)::value;
     const int64_t q = q0 + uq;
     if (q * GP >= nblk) return false;  // the same for every wave
-    // This wave's loads are group q's; after the barrier, every wave's are,
-    // and every wave has finished group q - 1.
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    // This wave's loads of group q have landed (those of the NG - 2 groups
+    // after it may not have); after the barrier every wave's have, and
+    // every wave has finished group q - 1, whose slots take group q + NG - 1.
+    __builtin_amdgcn_s_waitcnt(wait_vm((NG - 2) * GP * LPW));
     asm volatile("s_barrier" ::: "memory");
 #pragma unroll
-    for (int u = 0; u < GP; u++) issue((q + 1) * GP + u, ((uq + 1) % 2) * GP + u);
+    for (int u = 0; u < GP; u++) issue((q + NG - 1) * GP + u, ((uq + NG - 1) % NG) * GP + u);
     auto blockstep = [&](auto bc) __attribute__((always_inline)) -> bool {
       constexpr int u = decltype(bc)::value;
       const int64_t i = q * GP + u;
       if (i >= nblk) return false;
       if (i * kBlk < kmax_w)
-        compute(std::integral_constant<int, (uq % 2) * GP + u>{},
+        compute(std::integral_constant<int, (uq % NG) * GP + u>{},
                 std::integral_constant<int, (uq * GP + u) % 4>{}, i);
       return true;
     };
@@ -1269,7 +1272,7 @@ constexpr SdpaKernelFn mfma_kernel() {
   constexpr int WS = sdpa_shape_splits(V, SHAPE);
   if constexpr (SHAPE == SDPA_SHARED) {
     if constexpr (sdpa_shared_dims(D, V) && !MASK)
-      return sdpa_shared_kernel<T, D, V, sdpa_shared_waves(D, V), 2>;
+      return sdpa_shared_kernel<T, D, V, sdpa_shared_waves(D, V), 2, 2>;
     else
       return nullptr;
   } else if constexpr (SHAPE == SDPA_ROWS) {
