@@ -1022,55 +1022,82 @@ struct GemmTile {
     }
   }
 
-  // All CS chunk-steps of stage s (held in `sl`), operands of step j + 1 read
-  // while step j's MFMAs run; a group that ends inside the stage is folded
-  // right after its last chunk-step. GS (the group size) is a compile-time
-  // constant, so the fold positions are too.
+  // Register sets for P and X: groups are independent until their folds, so
+  // with groups no longer than a stage, NGR consecutive groups of a stage
+  // each get their own P and X. Their MFMAs issue back to back and their
+  // folds follow in ascending group order -- the same operations on the same
+  // values as folding each group right after its last chunk-step, without
+  // waiting for every group's products before the next group's MFMAs start.
+  // A power of two, bounded by about 80 registers of P and X (the 64 x 64
+  // footprint: two sets; four measured 7 % slower at group size 32).
   template <int GS>
+  static constexpr int q_sets() {
+    constexpr int ng = GS <= EPS ? EPS / GS : 1;
+    constexpr int per = (FN + 1) * FM * 4;  // registers of one group's P and X
+    int cap = 1;
+    while (2 * cap * per <= 80) cap *= 2;
+    return ng < cap ? ng : cap;
+  }
+
+  // All CS chunk-steps of stage s (held in `sl`), operands of step j + 1 read
+  // while step j's MFMAs run. With groups no longer than a stage, round r of
+  // the stage's groups (NGR of them) runs their chunk-steps into register
+  // sets 0 .. NGR - 1 and then folds them in ascending order. GS (the group
+  // size) is a compile-time constant, so the fold positions are too.
+  template <int GS, int NGR>
   __device__ __forceinline__ void q_compute_full(QSlot sl, int64_t s, f32x4_t (&acc)[FM][FN],
-                                                 f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
+                                                 f32x4_t (&P)[NGR][FM][FN],
+                                                 f32x4_t (&X)[NGR][FM]) const {
     constexpr int CPG = GS / 32;  // chunk-steps per group
     uint4 av[2][FM], bv[2][FN];
     read_operands(Slot{sl.a, sl.b}, 0, av[0], bv[0]);
 #pragma unroll
     for (int j = 0; j < CS; j++) {
       if (j + 1 < CS) read_operands(Slot{sl.a, sl.b}, j + 1, av[(j + 1) & 1], bv[(j + 1) & 1]);
-      // Inside a stage, a group starts at every CPG-th chunk-step when
-      // groups are no longer than stages; longer groups restart at the fold.
-      q_mfma(av[j & 1], bv[j & 1], GS <= EPS && j % CPG == 0, P, X);
       if constexpr (GS <= EPS) {
-        if ((j + 1) % CPG == 0) q_fold(sl, (j + 1) / CPG - 1, false, acc, P, X);
+        // Inside a stage a group starts at every CPG-th chunk-step.
+        const int gi = j / CPG;
+        q_mfma(av[j & 1], bv[j & 1], j % CPG == 0, P[gi % NGR], X[gi % NGR]);
+        if ((j + 1) % (CPG * NGR) == 0 || j + 1 == CS) {
+#pragma unroll
+          for (int q = gi - gi % NGR; q <= gi; q++) q_fold(sl, q, false, acc, P[q % NGR], X[q % NGR]);
+        }
+      } else {
+        q_mfma(av[j & 1], bv[j & 1], false, P[0], X[0]);
       }
     }
     if constexpr (GS > EPS) {
-      if ((((s + 1) * EPS) & (GS - 1)) == 0) q_fold(sl, 0, true, acc, P, X);
+      // Longer groups restart at the fold.
+      if ((((s + 1) * EPS) & (GS - 1)) == 0) q_fold(sl, 0, true, acc, P[0], X[0]);
     }
   }
 
-  // The first `steps` (< CS) chunk-steps of the last stage.
-  template <int GS>
+  // The first `steps` (< CS) chunk-steps of the last stage, one group at a
+  // time in register set 0.
+  template <int GS, int NGR>
   __device__ __forceinline__ void q_compute_part(QSlot sl, int64_t s, int steps,
-                                                 f32x4_t (&acc)[FM][FN], f32x4_t (&P)[FM][FN],
-                                                 f32x4_t (&X)[FM]) const {
+                                                 f32x4_t (&acc)[FM][FN], f32x4_t (&P)[NGR][FM][FN],
+                                                 f32x4_t (&X)[NGR][FM]) const {
 #pragma unroll
     for (int j = 0; j < CS - 1; j++) {
       if (j < steps) {
         uint4 av[FM], bv[FN];
         read_operands(Slot{sl.a, sl.b}, j, av, bv);
         const int64_t k_beg = (s * CS + j) * 32, k_end = k_beg + 32;
-        q_mfma(av, bv, (k_beg & (GS - 1)) == 0, P, X);
-        if ((k_end & (GS - 1)) == 0) q_fold(sl, (int)(k_end / GS - 1 - glo(s)), false, acc, P, X);
+        q_mfma(av, bv, (k_beg & (GS - 1)) == 0, P[0], X[0]);
+        if ((k_end & (GS - 1)) == 0)
+          q_fold(sl, (int)(k_end / GS - 1 - glo(s)), false, acc, P[0], X[0]);
       }
     }
   }
 
-  template <int GS>
+  template <int GS, int NGR>
   __device__ __forceinline__ void q_compute(QSlot sl, int64_t s, int steps, f32x4_t (&acc)[FM][FN],
-                                            f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
+                                            f32x4_t (&P)[NGR][FM][FN], f32x4_t (&X)[NGR][FM]) const {
     if (steps == CS)
-      q_compute_full<GS>(sl, s, acc, P, X);
+      q_compute_full<GS, NGR>(sl, s, acc, P, X);
     else if (steps > 0)
-      q_compute_part<GS>(sl, s, steps, acc, P, X);
+      q_compute_part<GS, NGR>(sl, s, steps, acc, P, X);
   }
 
   // Loads run QP stages ahead in registers; each stage is converted into one
@@ -1078,10 +1105,10 @@ struct GemmTile {
   // stages, so ring indices are compile-time). Before a slot is rewritten,
   // the barrier guarantees every wave finished reading it (LDS reads retire
   // before the barrier: lgkmcnt(0)).
-  template <bool COMPUTE, bool LOAD, int GS, typename QSlots>
+  template <bool COMPUTE, bool LOAD, int GS, int NGR, typename QSlots>
   __device__ __forceinline__ void q_rounds(const QSlots& slots, int64_t nst, int64_t nsteps,
                                            QStage (&q)[QP], f32x4_t (&acc)[FM][FN],
-                                           f32x4_t (&P)[FM][FN], f32x4_t (&X)[FM]) const {
+                                           f32x4_t (&P)[NGR][FM][FN], f32x4_t (&X)[NGR][FM]) const {
     for (int64_t s0 = 0; s0 < nst; s0 += QP) {
 #pragma unroll
       for (int u = 0; u < QP; u++) {
@@ -1092,7 +1119,7 @@ struct GemmTile {
           qload(s0 + u + 1 + QP, q[(u + 1) % QP]);
         }
         if constexpr (COMPUTE)
-          q_compute<GS>(slots(u & 1), s0 + u, steps_of(nsteps, s0 + u), acc, P, X);
+          q_compute<GS, NGR>(slots(u & 1), s0 + u, steps_of(nsteps, s0 + u), acc, P, X);
       }
     }
   }
@@ -1101,13 +1128,16 @@ struct GemmTile {
   __device__ __forceinline__ void main_loop_q(const QSlots& slots, int64_t nst, int64_t nsteps,
                                               bool computes, f32x4_t (&acc)[FM][FN]) const {
     static_assert(QP % 2 == 0, "ring of two LDS slots");
-    f32x4_t P[FM][FN], X[FM];
+    constexpr int NGR = q_sets<GS>();
+    f32x4_t P[NGR][FM][FN], X[NGR][FM];
 #pragma unroll
-    for (int i = 0; i < FM; i++) {
-      X[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < NGR; r++)
 #pragma unroll
-      for (int jn = 0; jn < FN; jn++) P[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
+      for (int i = 0; i < FM; i++) {
+        X[r][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jn = 0; jn < FN; jn++) P[r][i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
     QStage q[QP];
     if constexpr (QNT < NT) {
       // Loading waves stage every operand; computing waves only compute.
@@ -1116,11 +1146,11 @@ struct GemmTile {
         for (int u = 0; u < QP; u++) qload(u, q[u]);
         qstore(slots(0), q[0]);
         qload(QP, q[0]);
-        q_rounds<false, true, GS>(slots, nst, nsteps, q, acc, P, X);
+        q_rounds<false, true, GS, NGR>(slots, nst, nsteps, q, acc, P, X);
       } else if (computes) {
-        q_rounds<true, false, GS>(slots, nst, nsteps, q, acc, P, X);
+        q_rounds<true, false, GS, NGR>(slots, nst, nsteps, q, acc, P, X);
       } else {
-        q_rounds<false, false, GS>(slots, nst, nsteps, q, acc, P, X);
+        q_rounds<false, false, GS, NGR>(slots, nst, nsteps, q, acc, P, X);
       }
       return;
     }
@@ -1129,9 +1159,9 @@ struct GemmTile {
     qstore(slots(0), q[0]);
     qload(QP, q[0]);
     if (computes)
-      q_rounds<true, true, GS>(slots, nst, nsteps, q, acc, P, X);
+      q_rounds<true, true, GS, NGR>(slots, nst, nsteps, q, acc, P, X);
     else
-      q_rounds<false, true, GS>(slots, nst, nsteps, q, acc, P, X);
+      q_rounds<false, true, GS, NGR>(slots, nst, nsteps, q, acc, P, X);
   }
 
   // Register-staged path (unaligned operands): two slots, double buffered.
