@@ -241,6 +241,45 @@ def graph_us(torch, fn, calls=20, replays=7):
     return statistics.median(times)
 
 
+def feed_probe(torch, dev, reps=10):
+    """The per-CU operand feed that bounds the large-M GEMM (bi_feed_probe):
+    256 workgroups, one per CU, each stream 8 MB in 32 KB stages through the
+    256 x 256 footprints' LDS ring with no arithmetic, from one shared 2 MiB
+    panel (L2-resident after the first pass) and from 256 distinct 4 MiB
+    panels (HBM). A 256 x 256 tile consumes 32 KB per chunk-step of
+    2 * 256 * 256 * 32 flop, 31.8 B/clk per CU at the dense bf16 peak (4069
+    flop/clk per CU at 2.4 GHz), so feed / 31.8 bounds its MFMA fraction."""
+    from mlx_batch_invariant import _lib
+
+    L = _lib.lib()
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    stages, wgs = 256, 256
+    need = 32768 / (2.0 * 256 * 256 * 32 / (PEAK_BF16_TFLOPS * 1e12 / (256 * 2.4e9)))
+    out = {"bytes_per_clk_per_cu_needed_256x256": round(need, 1)}
+    for name, panel, panels in (("l2_shared_2MiB", 2 << 20, 1), ("hbm_256x4MiB", 4 << 20, 256)):
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()  # creates the HIP events
+            e1.record()
+            torch.cuda.synchronize()
+            _lib.check(L.bi_feed_probe(buf.data_ptr(), panel, panels, stages, wgs, e0.cuda_event,
+                                       e1.cuda_event, torch.cuda.current_stream().cuda_stream),
+                       "bi_feed_probe")
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        us = statistics.median(ts)
+        byts = float(wgs) * stages * 32768
+        bpc = byts / wgs / (us * 1e-6 * 2.4e9)
+        out[name] = {"us": round(us, 2), "gbps": round(byts / us / 1e3, 1),
+                     "bytes_per_clk_per_cu": round(bpc, 2),
+                     "mfma_frac_bound_256x256": round(bpc / need, 3)}
+    del buf
+    torch.cuda.empty_cache()
+    return out
+
+
 def prefill_gemms(torch, bi, dev, steps=8, warmup=3):
     """configs[4]'s prefill GEMMs at batch 8 x 512 tokens (M = 4096 rows),
     bi.linear on (N, K) weights, bf16: one step runs the four (K, N) shapes of
@@ -347,6 +386,8 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy three times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--feed-probe", action="store_true",
+                    help="only run the per-CU operand feed probe (bi_feed_probe) and print it")
     ap.add_argument("--prefill-shape", choices=("rows", "shared"),
                     help="only run the causal prefill (B=1, 32/8 heads, L=2048, D=128, bf16) "
                          "five times through one forced attention launch shape (for counter "
@@ -373,6 +414,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "copy", "bytes": src.numel() * 4}))
+        return
+    if args.feed_probe:
+        print(json.dumps({"feed_probe": feed_probe(torch, dev)}))
         return
     if args.prefill_shape:
         from mlx_batch_invariant import _attention, _lib
@@ -633,6 +677,7 @@ def main():
             differing += int((bits(bi.matmul(a[:b].contiguous(), w)[0]) != ref).sum())
 
     prefill_gemm = prefill_gemms(torch, bi, dev)
+    prefill_gemm["feed_probe"] = feed_probe(torch, dev)
     model = None if args.no_model else model_determinism(torch, bi, dev)
     cpu = None if args.no_cpu else cpu_baseline(ops)
 

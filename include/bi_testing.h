@@ -50,6 +50,18 @@ int bi_gemm_timed(const void* a, const void* b, const void* bias, void* out, int
                   int64_t N, int64_t K, int dtype, int trans_b, float alpha, float beta,
                   void* start_event, void* stop_event, void* hip_stream);
 
+/* Feed probe: the operand stream of a 256 x 256 GEMM footprint with no
+ * arithmetic. `workgroups` workgroups of 256 threads each stream `stages`
+ * stages of 32 KB through a 4-slot LDS ring by direct-to-LDS loads (8 of
+ * 1 KB per wave per stage, two stages in flight, a barrier per stage, as in
+ * the GEMM). Workgroup w reads panel w % panels of panel_bytes (a power of two,
+ * 32 KiB .. 1 GiB) at src; the caller provides panels * panel_bytes bytes.
+ * With one panel every pass after the first is served by the L2, so the rate
+ * is the per-CU operand feed from L2 that bounds the large-M GEMM. Timed like
+ * bi_gemm_timed (events may be NULL). No counterpart in the reference. */
+int bi_feed_probe(const void* src, int64_t panel_bytes, int panels, int stages, int workgroups,
+                  void* start_event, void* stop_event, void* hip_stream);
+
 /* bi_qgemm with the geometry forced to `g` (same arguments and semantics). */
 int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
                            const void* biases, void* out, int64_t M, int64_t N, int64_t K,

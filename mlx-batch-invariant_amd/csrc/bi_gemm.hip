@@ -251,6 +251,68 @@ extern "C" int bi_gemm_timed(const void* a, const void* b, const void* bias, voi
                 pick_for(a, b, M, N, K, dtype, trans_b), hip_stream, start_event, stop_event);
 }
 
+// ------------------------------------------------------------------ feed probe
+
+namespace {
+
+// The operand feed of a 256 x 256 footprint without its arithmetic: each
+// workgroup (4 waves; its 128 KB of LDS leave room for one per CU) streams
+// `stages` stages of 32 KB through a 4-slot LDS ring by direct-to-LDS loads,
+// 8 of 1 KB per wave per stage with two stages in flight and a barrier per
+// stage, as the GEMM's ring does, and does nothing with them. Workgroup w
+// reads panel w % panels (panel_bytes, a power of two) of src; stage s starts
+// at byte 32768 s of its panel, modulo the panel.
+__global__ void __launch_bounds__(256) feed_probe_kernel(const char* src, int64_t panel_bytes,
+                                                         int panels, int stages) {
+  __shared__ uint4 ring[4][2048];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const __amdgpu_buffer_rsrc_t r =
+      bi_gemm_dev::make_rsrc(src + (int64_t)(blockIdx.x % panels) * panel_bytes, panel_bytes);
+  const uint64_t mask = (uint64_t)panel_bytes - 1;
+  auto issue = [&](int64_t s, int slot) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int blk = i * 4 + w;
+      const uint32_t off = (uint32_t)(((uint64_t)s * 32768 + blk * 1024 + lane * 16) & mask);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (bi_gemm_dev::lds_void_t*)(&ring[slot][blk * 64]),
+                                               16, off, 0, 0, 0);
+    }
+  };
+  issue(0, 0);
+  issue(1, 1);
+  issue(2, 2);
+  for (int64_t s0 = 0; s0 < stages; s0 += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      __builtin_amdgcn_s_waitcnt(bi_gemm_dev::waitcnt_vm_lgkm0(16));
+      asm volatile("s_barrier" ::: "memory");
+      issue(s0 + u + 3, (u + 3) & 3);
+    }
+  }
+  // No load may still be landing in the LDS when the workgroup ends.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
+}  // namespace
+
+extern "C" int bi_feed_probe(const void* src, int64_t panel_bytes, int panels, int stages,
+                             int workgroups, void* start_event, void* stop_event,
+                             void* hip_stream) {
+  if (!src) return bi::fail(BI_EINVAL, "bi_feed_probe: null source");
+  if (panel_bytes < 32768 || panel_bytes > ((int64_t)1 << 30) || (panel_bytes & (panel_bytes - 1)))
+    return bi::fail(BI_EINVAL, "bi_feed_probe: panel_bytes must be a power of two in [32 KiB, 1 GiB]");
+  if (panels < 1 || stages < 1 || workgroups < 1)
+    return bi::fail(BI_EINVAL, "bi_feed_probe: panels, stages and workgroups must be positive");
+  hipExtLaunchKernelGGL(feed_probe_kernel, dim3((unsigned)workgroups), dim3(256), 0,
+                        static_cast<hipStream_t>(hip_stream), static_cast<hipEvent_t>(start_event),
+                        static_cast<hipEvent_t>(stop_event), 0, static_cast<const char*>(src),
+                        panel_bytes, panels, stages);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return bi::launch_error(e, "bi_feed_probe launch");
+  return BI_OK;
+}
+
 extern "C" int bi_gemm_num_geometries(void) { return kNumGeometries; }
 
 extern "C" int bi_gemm_geometry_info(int g, int* block_m, int* block_n, int* waves) {

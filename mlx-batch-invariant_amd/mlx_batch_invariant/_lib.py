@@ -44,6 +44,7 @@ SIGNATURES = {
                                        _c_int, _c_int, _c_float, _c_float, _c_int, _c_vp]),
     "bi_gemm_timed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                _c_int, _c_float, _c_float, _c_vp, _c_vp, _c_vp]),
+    "bi_feed_probe": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
     "bi_qgemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                           _c_int, _c_int, _c_vp]),
     "bi_qgemm_with_geometry": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
