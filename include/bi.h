@@ -110,7 +110,10 @@ int bi_gemm(const void* a, const void* b, const void* bias, void* out,
  * them, _attention.py:92-98). The matrix-core path multiplies the values of a
  * key that is visible to another query row of the same 32-key block, but not
  * to this one, by zero; a NaN or infinity there, which reaches that other
- * row's output in any case, also reaches this row's.
+ * row's output in any case, may also reach this row's, as an all-NaN row,
+ * depending on the launch shape and on which rows share its workgroup. Bit
+ * parity across launch shapes, batch sizes and query lengths therefore holds
+ * for finite values of every key that some query row of the call can see.
  * Supported head dims (D, V): D == V in {32, 64, 96, ..., 512} (every multiple
  * of 32 up to 512) and (192, 128), (128, 64), (64, 128), (256, 128), (128, 256),
  * (576, 512); other multiples of 32 return BI_EUNSUPPORTED (each pair is a

@@ -297,6 +297,37 @@ def test_unwritten_cache_tail_never_reaches_the_output(cuda, dname, dtype):
             assert np.array_equal(bits(got), bits(want)), case
 
 
+@pytest.mark.parametrize("dname,dtype", LOW)
+def test_nan_value_hidden_from_some_rows_by_the_causal_mask(cuda, dname, dtype):
+    """A NaN value row at key j of a start-aligned causal prefill (qL = N):
+    rows s >= j see it and are all NaN in every launch shape; a row s < j
+    cannot see it, and is either bitwise its result with a finite value there
+    or all NaN, by launch shape and by which rows share its workgroup and
+    32-key block (its zero probability multiplies the value: 0 * NaN = NaN).
+    So bit parity across shapes holds for finite values of the keys some row
+    of the call can see (include/bi.h); the reference skips such a key per
+    row (_attention.py:92-98)."""
+    B, H, Hkv, D, L, j = 1, 8, 2, 128, 96, 40
+    q = rn((B, H, L, D), dtype, 131, device=cuda)
+    k = rn((B, Hkv, L, D), dtype, 132, device=cuda)
+    v = rn((B, Hkv, L, D), dtype, 133, device=cuda)
+    vn = v.clone()
+    vn[:, :, j] = float("nan")
+    leaked = {}
+    for shape in shapes_for(dtype, D, D, H // Hkv):
+        want = bits(run(q, k, v, "start", shape)).reshape(B, H, L, D)
+        out = run(q, k, vn, "start", shape)
+        got = bits(out).reshape(B, H, L, D)
+        nan_rows = torch.isnan(out).all(-1).cpu().numpy()
+        assert nan_rows[:, :, j:].all(), (dname, shape)
+        same = (got == want).all(-1)
+        assert (nan_rows | same)[:, :, :j].all(), (dname, shape)
+        leaked[shape] = int(nan_rows[:, :, :j].sum())
+    # Every matrix-core shape ran (how many rows before j turn NaN is the
+    # shape's business; the finite ones are exact).
+    assert len(leaked) >= 5, leaked
+
+
 @pytest.mark.parametrize("D,V", PAIRS)
 def test_head_dims_accuracy_and_query_length_invariance(cuda, D, V):
     """Every built (D, V) pair (the reference takes any multiples of 32,
