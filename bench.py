@@ -13,13 +13,24 @@ resident in HBM. Alongside, on the same run:
   * stock torch.matmul (hipBLASLt) on the same inputs, interleaved;
   * the same sweep in f16 and fp32 (fp32 against the 157.3 TFLOP/s fp32
     MFMA peak);
-  * decode SDPA (configs[2]: B = 64, 32/8 heads, D = 128, N = 8192) GB/s, and
-    a decode sweep over B in {1, 8, 64} x N in {2048, 8192};
+  * a sustained leg: the same step repeated for SUSTAINED_S seconds, its
+    dominant launch self-timed in every 16th step (roofline.sustained);
+  * decode SDPA (configs[2]: B = 64, 32/8 heads, D = 128, N = 8192) GB/s, a
+    decode sweep over B in {1, 8, 64} x N in {2048, 8192} (eager calls, against
+    stock), and graph-timed cells B in {1, 2, 4, 8} x N in {2048, 8192} (20
+    calls replayed as one HIP graph: device time, where eager calls of these
+    sizes are bound by the host's per-call cost);
   * causal prefill SDPA (B = 1, 32/8 heads, D = 128, 2048 x 2048) TFLOP/s,
     against stock torch SDPA;
+  * the configs[4] prefill GEMMs at M = 4096 (bi.linear on (N, K) weights,
+    against stock F.linear, each launch timed inside the steps) against the
+    MFMA peak, and the feed probe (bi_feed_probe: the GEMM ring's operand
+    stream with no arithmetic, from L2 and from HBM);
   * 4-bit affine quantized linear (4096 x 4096, group 64) at M = 1 and 256,
     against stock dequantize + F.linear;
   * a bit-invariance check of row 0 of every shape across batch sizes 1..256;
+  * the configs[4] decoder's prefill at batch 8 and the bits of sequence 0's
+    logits against batch 1, invariant and stock (--no-model skips it);
   * the CPU baseline on the host cores this process may use: the oracle's
     fixed-order fp32 restatements of the reference GEMM and attention (C,
     OpenMP) on bounded samples of the same workloads, beside stock torch.
