@@ -13,7 +13,7 @@ resident in HBM. Alongside, on the same run:
   * stock torch.matmul (hipBLASLt) on the same inputs, interleaved;
   * the same sweep in f16 and fp32 (fp32 against the 157.3 TFLOP/s fp32
     MFMA peak);
-  * a sustained leg: the same step repeated for SUSTAINED_S seconds, its
+  * a sustained leg: the same step repeated for --sustained seconds, its
     dominant launch self-timed in every 16th step (roofline.sustained);
   * decode SDPA (configs[2]: B = 64, 32/8 heads, D = 128, N = 8192) GB/s, a
     decode sweep over B in {1, 8, 64} x N in {2048, 8192} (eager calls, against
@@ -222,6 +222,11 @@ def cpu_sdpa_baseline(torch, np):
             "torch_cpu_gbps": round(by * tpasses / tdt / 1e9, 3)}
 
 
+def progress(leg):
+    """One stderr line as each leg starts (the JSON line stays alone on stdout)."""
+    print("bench.py: %s" % leg, file=sys.stderr, flush=True)
+
+
 def graph_us(torch, fn, calls=20, replays=7):
     """Device time of one fn() call: `calls` calls captured in a HIP graph,
     replayed `replays` times between HIP events; median replay / calls."""
@@ -394,6 +399,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the 32-layer decoder determinism check (configs[4])")
+    ap.add_argument("--sustained", type=float, default=SUSTAINED_S, metavar="SECONDS",
+                    help="length of the sustained leg (default %(default)s s; 0: as many steps "
+                         "as the burst, e.g. for counter passes, where every dispatch is "
+                         "serialised with its counter readout)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy three times (the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -452,6 +461,7 @@ def main():
             if outs is not None:
                 outs.append(y)
 
+    progress("steps")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -485,12 +495,13 @@ def main():
     value = step_flops * args.steps / elapsed / 1e12
     dom_us = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs.values()) * 1e3
 
-    # Sustained: the same step repeated for at least SUSTAINED_S seconds (the
+    progress("sustained")
+    # Sustained: the same step repeated for at least --sustained seconds (the
     # burst above covers a few milliseconds; the dominant kernel slows by
     # several per cent under longer load), the dominant launch self-timed in
     # every 16th step.
-    n_sus = max(args.steps, int(math.ceil(SUSTAINED_S * 1e3 / ms_per_step)))
-    sus_timed = list(range(8, n_sus, 16))
+    n_sus = max(args.steps, int(math.ceil(args.sustained * 1e3 / ms_per_step)))
+    sus_timed = list(range(min(8, n_sus // 2), n_sus, 16))
     sus_evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in sus_timed]
     for e0, e1 in sus_evs:
@@ -510,6 +521,7 @@ def main():
     sus_us = [e0.elapsed_time(e1) * 1e3 for e0, e1 in sus_evs]
     q4 = sus_us[len(sus_us) * 3 // 4:]
 
+    progress("per-shape")
     # Per-shape and stock comparison (HIP events, interleaved A/B, median of 9).
     def time_us(fn, reps=20):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -537,6 +549,7 @@ def main():
                           "geometry": _gemm.geometries()[
                               _gemm._lib.lib().bi_gemm_pick_geometry(M, N, K, 2, 0)]})
 
+    progress("f16/fp32 sweep")
     # The same sweep in f16 and fp32 (fp32 against its own MFMA peak): HIP
     # events around whole steps, after a warmup.
     other_dtypes = {}
@@ -584,6 +597,7 @@ def main():
                                                      PEAK_HBM_GBS, 4),
                           "launches_timed": len(sus_us)}}
 
+    progress("decode attention")
     # Decode SDPA.
     g = torch.Generator().manual_seed(0)
     B, H, Hkv, N, D = SDPA["B"], SDPA["H"], SDPA["Hkv"], SDPA["N"], SDPA["D"]
@@ -621,6 +635,7 @@ def main():
                           "stock_us": round(t_st, 1)})
             del qd, kd, vd
     sdpa["sweep"] = sweep
+    progress("graph-timed decode")
     # Small batches, graph-timed: 20 calls captured in a HIP graph and
     # replayed, so the figure is device time (eager calls at these sizes are
     # bound by the host's per-call cost).
@@ -638,6 +653,7 @@ def main():
             del qd, kd, vd
     sdpa["graph_timed"] = graph_cells
 
+    progress("prefill attention")
     # Causal prefill attention (the query-row-blocked path of the same kernel):
     # B=1, 32/8 heads, D=128, 2048 query rows over 2048 keys.
     L = 2048
@@ -658,6 +674,7 @@ def main():
                             "frac_of_min_roof": round(pf_flops / pf_bi / 1e6 / pf_roof, 4),
                             "mfma_frac": round(pf_flops / pf_bi / 1e6 / PEAK_BF16_TFLOPS, 4)}}
 
+    progress("quantized linear")
     # Affine 4-bit quantized linear (group 64), 4096 x 4096 weight: decode and
     # M=256 rows; stock is dequantize + F.linear.
     wq = (torch.randn(4096, 4096, generator=g) / 64).to(torch.bfloat16)
@@ -679,6 +696,7 @@ def main():
                              "tflops": round(q_flops / q_bi / 1e6, 2),
                              "frac_of_min_roof": round(q_flops / q_bi / 1e6 / q_roof, 4)}
 
+    progress("invariance check")
     # Invariance spot check: row 0 of every shape of the sweep across batch
     # sizes 1..256 (each batch size picks its own workgroup footprint).
     differing = 0
@@ -687,9 +705,14 @@ def main():
         for b in (2, 3, 8, 16, 17, 33, 64, 65, 128, 255, 256):
             differing += int((bits(bi.matmul(a[:b].contiguous(), w)[0]) != ref).sum())
 
+    progress("M=4096 GEMMs and feed probe")
     prefill_gemm = prefill_gemms(torch, bi, dev)
     prefill_gemm["feed_probe"] = feed_probe(torch, dev)
+    if not args.no_model:
+        progress("model determinism")
     model = None if args.no_model else model_determinism(torch, bi, dev)
+    if not args.no_cpu:
+        progress("CPU baseline")
     cpu = None if args.no_cpu else cpu_baseline(ops)
 
     line = {
