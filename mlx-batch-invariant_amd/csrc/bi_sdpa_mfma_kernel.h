@@ -633,7 +633,6 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
               bm = use[kt][e] ? fmaxf(bm, sv) : bm;
               used |= use[kt][e] ? 1u << (4 * kt + e) : 0u;
             }
-          bm = col_max(bm);
         } else {
           // Rounding is monotonic: the largest raw score, scaled, is the
           // largest scaled score.
@@ -641,13 +640,22 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
           for (int kt = 0; kt < 2; kt++)
 #pragma unroll
             for (int e = 0; e < 4; e++) bm = use[kt][e] ? fmaxf(bm, r[kt][e]) : bm;
-          bm = col_max(bm) * p.ascale2;
         }
-        const bool any = bm > -INFINITY;
         // The base moves only when the block's largest score passes it by more
         // than 8 (p then stays <= 2^8): few rescales, the same result after o / l.
-        const float mn = (any && bm > m[ct] + 8.f) ? bm : m[ct];
-        f[ct] = mn == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - mn);
+        // The column's largest score is one of its four lanes' maxima, so it
+        // moves iff one of those lanes' own maxima (scaled) passes m + 8, by
+        // the same product and compare; when no lane of the wave does, every
+        // column keeps m and f = 1 without the cross-lane maximum.
+        const float m8 = m[ct] + 8.f;
+        float mn = m[ct];
+        f[ct] = 1.f;
+        if (__builtin_amdgcn_ballot_w64((MK ? bm : bm * p.ascale2) > m8) != 0) {  // wave-uniform
+          bm = MK ? col_max(bm) : col_max(bm) * p.ascale2;
+          const bool any = bm > -INFINITY;
+          mn = (any && bm > m8) ? bm : m[ct];
+          f[ct] = mn == m[ct] ? 1.f : __builtin_amdgcn_exp2f(m[ct] - mn);
+        }
         float pv[2][4];
         float ps = 0.f;
 #pragma unroll
@@ -1145,10 +1153,20 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
           use[kt][e] = FULL || key0 + 16 * kt + e < kend;
           bm = use[kt][e] ? fmaxf(bm, sc[kt][e]) : bm;
         }
-      bm = col_max(bm) * p.ascale2;
-      const bool any = bm > -INFINITY;
-      const float mn = (any && bm > m[c] + 8.f) ? bm : m[c];
-      f = mn == m[c] ? 1.f : __builtin_amdgcn_exp2f(m[c] - mn);
+      // The column's maximum is one of its four lanes' maxima, so the column
+      // moves its base iff one of its lanes' own scaled maxima exceeds
+      // m + 8 (the same product, the same compare). When no lane of the
+      // wave does, every column keeps m and f = 1 without the cross-lane
+      // maximum; otherwise the full step runs, with the same result.
+      const float m8 = m[c] + 8.f;
+      float mn = m[c];
+      f = 1.f;
+      if (__builtin_amdgcn_ballot_w64(bm * p.ascale2 > m8) != 0) {  // wave-uniform
+        bm = col_max(bm) * p.ascale2;
+        const bool any = bm > -INFINITY;
+        mn = (any && bm > m8) ? bm : m[c];
+        f = mn == m[c] ? 1.f : __builtin_amdgcn_exp2f(m[c] - mn);
+      }
       float pv[2][4];
       float ps = 0.f;
 #pragma unroll
