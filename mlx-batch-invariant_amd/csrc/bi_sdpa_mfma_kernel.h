@@ -196,6 +196,22 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t byt
                                            0x00020000);
 }
 
+// As make_rsrc for a byte count already in [0, 2^31); clamp31 caps a
+// positive count there.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc_n(const void* base, uint32_t n) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, (int)__builtin_amdgcn_readfirstlane(n),
+                                           0x00020000);
+}
+// (The shifted count is truncated to 32 bits so that the test stays a 32-bit
+// scalar compare; the count is never negative.)
+__device__ __forceinline__ uint32_t clamp31(int64_t bytes) {
+  return (uint32_t)((uint64_t)bytes >> 31) != 0 ? 0x7FFFFFFFu : (uint32_t)bytes;
+}
+
 // Sum / max over the four lanes of a column (lanes r, r + 16, r + 32, r + 48,
 // one per 16-lane row). permlane16_swap pairs rows (0, 1) and (2, 3),
 // permlane32_swap the two halves; every lane adds its pair's operands in the
@@ -950,18 +966,26 @@ struct Shared {
   struct Loads {
     const T* kb;
     const T* vb;
-    int64_t ks2, vs2, kmax, nblk;
+    // The next block's first key and value rows, the bytes from there to
+    // the end of the last row some column sees, 32 rows in bytes, and the
+    // blocks left to load (issue() walks the blocks in order).
+    const char* kp;
+    const char* vp;
+    int64_t krem, vrem, kstep, vstep;
+    int left;
     uint32_t loff[LPW];
     bool lkey[LPW];
-    __device__ __forceinline__ void init(const SdpaArgs& p, int64_t b, int64_t kvh, int64_t kmax_,
-                                         int64_t nblk_, int wave, int lane) {
+    __device__ __forceinline__ void init(const SdpaArgs& p, int64_t b, int64_t kvh, int64_t kmax,
+                                         int nblk, int wave, int lane) {
       constexpr uint32_t E = sizeof(T);
-      kb = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
-      vb = static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
-      ks2 = p.ks[2];
-      vs2 = p.vs[2];
-      kmax = kmax_;
-      nblk = nblk_;
+      const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
+      kp = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1]);
+      vp = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1]);
+      krem = ((kmax - 1) * ks2 + D) * E;
+      vrem = ((kmax - 1) * vs2 + V) * E;
+      kstep = kBlk * ks2 * E;
+      vstep = kBlk * vs2 * E;
+      left = nblk;
 #pragma unroll
       for (int u = 0; u < LPW; u++) {
         const int j = wave * LPW + u;
@@ -975,19 +999,22 @@ struct Shared {
         }
       }
     }
-    // This wave's loads of block i into the slot at dst (the slot's first
-    // uint4 plus this wave's first load).
-    __device__ __forceinline__ void issue(int64_t i, uint4* dst) const {
-      const int64_t key0 = i * kBlk;
-      const bool in = i < nblk;
-      const auto rk = make_rsrc(kb + (in ? key0 * ks2 : 0),
-                                in ? ((kmax - key0 - 1) * ks2 + D) * (int64_t)sizeof(T) : 0);
-      const auto rv = make_rsrc(vb + (in ? key0 * vs2 : 0),
-                                in ? ((kmax - key0 - 1) * vs2 + V) * (int64_t)sizeof(T) : 0);
+    // This wave's loads of the next block into the slot at dst (the slot's
+    // first uint4 plus this wave's first load). While blocks are left, the
+    // remaining byte counts are at least one row (D or V elements).
+    __device__ __forceinline__ void issue(uint4* dst) {
+      const bool in = left > 0;
+      const auto rk = make_rsrc_n(kp, in ? clamp31(krem) : 0u);
+      const auto rv = make_rsrc_n(vp, in ? clamp31(vrem) : 0u);
 #pragma unroll
       for (int u = 0; u < LPW; u++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(lkey[u] ? rk : rv, (lds_void_t*)(dst + u * 64),
                                                  16, (int)loff[u], 0, 0, 0);
+      kp += kstep;
+      vp += vstep;
+      krem -= kstep;
+      vrem -= vstep;
+      left--;
     }
   };
 };
@@ -1024,14 +1051,16 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
   };
   const int64_t last_cc = (c0 + COLS < ncol ? c0 + COLS : ncol) - 1;
   const int64_t kmax = kend_of(last_cc / G);  // keys some column of the workgroup sees
-  const int64_t nblk = (kmax + kBlk - 1) / kBlk;
-  // This wave's columns w0 .. w0 + 15: the keys the last of them sees, and
-  // those every one of them sees.
+  // Block counts and indices fit in 32 bits (the host bounds N below
+  // 2^31 - 1024), which keeps the loop's compares on the scalar unit.
+  const int nblk = (int)((kmax + kBlk - 1) / kBlk);
+  // This wave's columns w0 .. w0 + 15: the blocks holding a key the last of
+  // them sees, and the blocks whose keys every one of them sees.
   const int64_t w0 = c0 + 16 * wave;
   const bool wany = w0 < ncol;
   const int64_t wlast = (w0 + 16 < ncol ? w0 + 16 : ncol) - 1;
-  const int64_t kmax_w = wany ? kend_of(wlast / G) : 0;
-  const int64_t kfull_w = wany ? kend_of(w0 / G) : 0;
+  const int nvis_w = wany ? (int)((kend_of(wlast / G) + kBlk - 1) / kBlk) : 0;
+  const int nfull_w = wany ? (int)(kend_of(w0 / G) / kBlk) : 0;
 
   // This lane's column, its query as the B operand of the score MFMAs
   // (Q[col][32i + 8g ..]), and the 4 chains' state.
@@ -1059,9 +1088,10 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
 
   typename C::Loads ld;
   ld.init(p, b, kvh, kmax, nblk, wave, lane);
-  // Block i of group h (0 .. NG - 1) into slot h * GP + i mod GP.
-  auto issue = [&](int64_t i, int slot) __attribute__((always_inline)) {
-    ld.issue(i, ring + slot * C::SLOT + wave * LPW * 64);
+  // The next block (blocks are issued in order; block i of group h,
+  // 0 .. NG - 1, goes to slot h * GP + i mod GP).
+  auto issue = [&](int slot) __attribute__((always_inline)) {
+    ld.issue(ring + slot * C::SLOT + wave * LPW * 64);
   };
 
   // LDS lane addresses in slot 0 of each group: lane (r16, g) reads chunk
@@ -1095,7 +1125,7 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
 
   // One block of chain c from slot `slot` (its loads have landed for every
   // wave: the caller waited and synchronised).
-  auto compute = [&](auto slot_c, auto chain, int64_t blk) __attribute__((always_inline)) {
+  auto compute = [&](auto slot_c, auto chain, int blk) __attribute__((always_inline)) {
     constexpr int c = decltype(chain)::value;
     constexpr int slot = decltype(slot_c)::value;
     constexpr int h = slot * C::SLOT * 16 / 65536;
@@ -1139,7 +1169,7 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
         va[db][kt] = ds_read_tr_at(vofs[h][db], SOFF + kt * 16 * VCH * 16);
     // Softmax of chain c over the block (the per-column steps of
     // sdpa_mfma_kernel, in the same order).
-    const int key0 = (int)blk * kBlk + 4 * g;
+    const int key0 = blk * kBlk + 4 * g;
     uint2 ph[2];
     float f;
     auto softmax = [&](auto full_tag) __attribute__((always_inline)) {
@@ -1182,7 +1212,7 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) ph[kt] = pack_p<T>(pv[kt]);
     };
-    if ((blk + 1) * kBlk <= kfull_w)
+    if (blk < nfull_w)
       softmax(std::true_type{});
     else
       softmax(std::false_type{});
@@ -1210,11 +1240,11 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
   // so slot and chain indices are compile-time.
   constexpr int UG = lcm(NG, GP >= 4 ? 1 : 4 / GP);
 #pragma unroll
-  for (int u = 0; u < (NG - 1) * GP; u++) issue(u, u);
-  int64_t q0 = 0;
+  for (int u = 0; u < (NG - 1) * GP; u++) issue(u);
+  int q0 = 0;
   auto group = [&](auto qc) __attribute__((always_inline)) -> bool {
     constexpr int uq = decltype(qc)::value;
-    const int64_t q = q0 + uq;
+    const int q = q0 + uq;
     if (q * GP >= nblk) return false;  // the same for every wave
     // This wave's loads of group q have landed (those of the NG - 2 groups
     // after it may not have); after the barrier every wave's have, and
@@ -1222,12 +1252,12 @@ __global__ void __launch_bounds__(64 * NW) sdpa_shared_kernel(SdpaArgs p) {
     __builtin_amdgcn_s_waitcnt(wait_vm((NG - 2) * GP * LPW));
     asm volatile("s_barrier" ::: "memory");
 #pragma unroll
-    for (int u = 0; u < GP; u++) issue((q + NG - 1) * GP + u, ((uq + NG - 1) % NG) * GP + u);
+    for (int u = 0; u < GP; u++) issue(((uq + NG - 1) % NG) * GP + u);
     auto blockstep = [&](auto bc) __attribute__((always_inline)) -> bool {
       constexpr int u = decltype(bc)::value;
-      const int64_t i = q * GP + u;
+      const int i = q * GP + u;
       if (i >= nblk) return false;
-      if (i * kBlk < kmax_w)
+      if (i < nvis_w)
         compute(std::integral_constant<int, (uq % NG) * GP + u>{},
                 std::integral_constant<int, (uq * GP + u) % 4>{}, i);
       return true;
