@@ -183,21 +183,10 @@ __device__ inline int xcd_remap(int w, int total) {
   return w;
 }
 
-// Buffer resource over [base, base + bytes) (wave-uniform): loads past the
-// end return zeros without touching memory.
-__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  constexpr int64_t kMax = 0x7FFFFFFF;
-  const int32_t n = bytes <= 0 ? 0 : (int32_t)(bytes < kMax ? bytes : kMax);
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, __builtin_amdgcn_readfirstlane(n),
-                                           0x00020000);
-}
-
-// As make_rsrc for a byte count already in [0, 2^31); clamp31 caps a
-// positive count there.
+// Buffer resource over [base, base + n) (wave-uniform, n below 2^31): loads
+// past the end return zeros without touching memory. clamp31 caps a byte
+// count that is never negative at 2^31 - 1 (the shifted count is truncated
+// to 32 bits, so the test stays a 32-bit scalar compare).
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc_n(const void* base, uint32_t n) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
@@ -206,8 +195,6 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc_n(const void* base, uint32_t 
   return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, (int)__builtin_amdgcn_readfirstlane(n),
                                            0x00020000);
 }
-// (The shifted count is truncated to 32 bits so that the test stays a 32-bit
-// scalar compare; the count is never negative.)
 __device__ __forceinline__ uint32_t clamp31(int64_t bytes) {
   return (uint32_t)((uint64_t)bytes >> 31) != 0 ? 0x7FFFFFFFu : (uint32_t)bytes;
 }
@@ -306,7 +293,8 @@ struct Chain {
   const T* kb;
   const T* vb;
   const T* mb;
-  int64_t ks2, vs2, N, nit, mext;
+  int64_t ks2, vs2, N, mext;
+  int nit;
   int wave;
   // Lane byte offsets: key row 16kt + r16 at dims 8g ..; value chunk j;
   // mask keys 4g .. of the lane's row in each column tile. The other key and
@@ -321,7 +309,7 @@ struct Chain {
   // zeros: their p is +0 in every column, and their values never reach o,
   // whatever they hold (the reference never reads them, _attention.py:92-93).
   __device__ __forceinline__ void init(const SdpaArgs& p, int64_t b, int64_t kvh, int ws, int w,
-                                       int64_t n_it, int lane, const int64_t* mrow, int64_t kmax) {
+                                       int n_it, int lane, const int64_t* mrow, int64_t kmax) {
     constexpr uint32_t E = sizeof(T);
     const int g = lane >> 4, r16 = lane & 15;
     kb = static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1];
@@ -354,12 +342,13 @@ struct Chain {
     }
   }
   // Rows key0 .. N - 1 of a stream whose rows hold `row` elements.
+  // (Blocks i < nit start below N, so the byte count is at least one row.)
   __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const T* base, int64_t stride, int row,
-                                                         int64_t i) const {
-    const int64_t key0 = (wave + kWaves * i) * kBlk;
+                                                         int i) const {
+    const int64_t key0 = (int64_t)(wave + kWaves * i) * kBlk;
     const bool in = i < nit;
-    return make_rsrc(base + (in ? key0 * stride : 0),
-                     in ? ((N - key0 - 1) * stride + row) * (int64_t)sizeof(T) : 0);
+    return make_rsrc_n(base + (in ? key0 * stride : 0),
+                       in ? clamp31(((N - key0 - 1) * stride + row) * (int64_t)sizeof(T)) : 0u);
   }
   // Keys of block i into the score MFMAs' A operands: lane (r16, g) holds
   // K[16kt + r16][32q + 8g .. + 7]. Mask values: those of the lane's keys
@@ -371,10 +360,10 @@ struct Chain {
   struct MRegs {
     unsigned short m[CT][8];
   };
-  __device__ __forceinline__ void mload(int64_t i, unsigned short (&m)[CT][8]) const {
-    const int64_t key0 = (wave + kWaves * i) * kBlk;
-    const bool in = i < nit;
-    const auto rm = make_rsrc(mb + (in ? key0 : 0), in ? (mext - key0) * (int64_t)sizeof(T) : 0);
+  __device__ __forceinline__ void mload(int i, unsigned short (&m)[CT][8]) const {
+    const int64_t key0 = (int64_t)(wave + kWaves * i) * kBlk;
+    const bool in = i < nit;  // then key0 < N <= mext
+    const auto rm = make_rsrc_n(mb + (in ? key0 : 0), in ? clamp31((mext - key0) * (int64_t)sizeof(T)) : 0u);
 #pragma unroll
     for (int ct = 0; ct < CT; ct++)
 #pragma unroll
@@ -382,7 +371,7 @@ struct Chain {
         m[ct][j] = __builtin_amdgcn_raw_buffer_load_b16(
             rm, (int)(moff[ct] + (16 * (j >> 2) + (j & 3)) * sizeof(T)), 0, 0);
   }
-  __device__ __forceinline__ void kload(int64_t i, KRegs& kr) const {
+  __device__ __forceinline__ void kload(int i, KRegs& kr) const {
     if constexpr (!KL) {
       const auto rs = rsrc(kb, ks2, D, i);
 #pragma unroll
@@ -397,7 +386,7 @@ struct Chain {
   }
   // Keys (KL) and values of block i into an LDS slot (loads that write LDS
   // directly; the keys of a slot first, then its values).
-  __device__ __forceinline__ void vload(int64_t i, uint4* dst) const {
+  __device__ __forceinline__ void vload(int i, uint4* dst) const {
     // The slot's previous reads have returned before new data lands.
     __builtin_amdgcn_s_waitcnt(kWaitLds);
     if constexpr (KL) {
@@ -464,8 +453,10 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
   };
   const int64_t last_cc = (c0 + COLS < ncol ? c0 + COLS : ncol) - 1;
   const int64_t kmax = kend_of(last_cc / G);  // keys some column of the workgroup sees
-  const int64_t nblk = (kmax + kBlk - 1) / kBlk;
-  const int64_t kfull = kend_of(c0 / G);  // keys every column of the workgroup sees
+  // Block counts and indices fit in 32 bits (the host bounds N below
+  // 2^31 - 1024), which keeps the loop's compares on the scalar unit.
+  const int nblk = (int)((kmax + kBlk - 1) / kBlk);
+  const int nfull = (int)(kend_of(c0 / G) / kBlk);  // blocks every column of the workgroup sees
 
   // This lane's column in each tile; its query as the B operand of the score
   // MFMAs (Q[col][32i + 8g ..]); its chain state.
@@ -498,7 +489,7 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
   // block's first row, so the lane offsets below are the same for every block
   // (and below 2^31: the host bounds 32 * stride).
   // This chain's blocks are wave + 4i, i < nit.
-  const int64_t nit = nblk > wave ? (nblk - wave + kWaves - 1) / kWaves : 0;
+  const int nit = nblk > wave ? (nblk - wave + kWaves - 1) / kWaves : 0;
   const int wslot = wave * C::VSLOT;  // this wave's slot within each array
   C ld;
   ld.init(p, b, kvh, ws, wave, nit, lane, mrow, kmax);
@@ -508,10 +499,10 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
   // j - 1, so there are nit0 + 1 steps and blocks are issued SV - 2 steps
   // ahead; otherwise step j computes block j, issued SV - 1 steps ahead
   // (two steps at the slot counts built, three and four).
-  const int64_t nit0 = nblk > 0 ? (nblk + kWaves - 1) / kWaves : 0;
+  const int nit0 = nblk > 0 ? (nblk + kWaves - 1) / kWaves : 0;
   constexpr bool PIPE = LW != 0 && SV >= 4;
   constexpr int AHEAD = PIPE ? SV - 2 : SV - 1;
-  const int64_t steps = PIPE ? nit0 + 1 : nit0;
+  const int steps = PIPE ? nit0 + 1 : nit0;
   if constexpr (LW != 0) {
     if (loader) {
       // Block j lands in slot j % SV. Before barrier j this wave waits for
@@ -522,7 +513,7 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
       // whose values were read at step j - 1; else block j - 1).
 #pragma unroll
       for (int u = 0; u < AHEAD; u++) ld.vload(u, arr(u) + wslot);
-      for (int64_t j0 = 0; j0 < steps; j0 += SV) {
+      for (int j0 = 0; j0 < steps; j0 += SV) {
 #pragma unroll
         for (int u = 0; u < SV; u++) {
           if (j0 + u >= steps) break;
@@ -610,11 +601,11 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
   // VPRE, already issued by the caller (asm LDS reads only).
   constexpr int MKCT = MK ? CT : 1;
   auto update = [&](auto vpre, const f32x4_t (&sc)[CT][2], const unsigned short (&mk)[MKCT][8],
-                    int slot, int64_t blk, VA_t& va) __attribute__((always_inline)) {
+                    int slot, int blk, VA_t& va) __attribute__((always_inline)) {
     constexpr bool VPRE = decltype(vpre)::value;
     static_assert(!VPRE || C::ASM_TR, "values read ahead by asm reads only");
     // Key indices fit in 32 bits (the host checks N < 2^31).
-    const int key0 = (int)blk * kBlk + 4 * g;
+    const int key0 = blk * kBlk + 4 * g;
     uint2 ph[CT][2];
     float f[CT];
     uint32_t used = 0;  // mask: bit 4kt + e set if this lane's column uses key 16kt + 4g + e
@@ -690,7 +681,7 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
         for (int kt = 0; kt < 2; kt++) ph[ct][kt] = pack_p<T>(pv[kt]);
       }
     };
-    if (!MK && (blk + 1) * kBlk <= kfull)
+    if (!MK && blk < nfull)
       softmax(std::true_type{});
     else
       softmax(std::false_type{});
@@ -758,7 +749,7 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
   // One block of this chain: keys in kr (or, KL, in slot `slot` beside the
   // values, landed with at most VWAIT younger operations in flight).
   auto compute = [&](const typename C::KRegs& kr, const unsigned short (&mk)[MKCT][8], int slot,
-                     int64_t blk) __attribute__((always_inline)) {
+                     int blk) __attribute__((always_inline)) {
     KL_t kl;
     if constexpr (KL) {
       __builtin_amdgcn_s_waitcnt(wait_vm(C::VWAIT));
@@ -784,10 +775,10 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
     // previous step left in sp) finishes: the two are independent, so each
     // hides the other's latency. Every product is the one compute() makes.
     f32x4_t sp[CT][2];
-    for (int64_t j0 = 0; j0 < steps; j0 += SV) {
+    for (int j0 = 0; j0 < steps; j0 += SV) {
 #pragma unroll
       for (int u = 0; u < SV; u++) {
-        const int64_t j = j0 + u;
+        const int j = j0 + u;
         if (j >= steps) break;
         asm volatile("s_barrier" ::: "memory");
         // From step nit on, the slot's stale keys are read and scored too
@@ -808,10 +799,10 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
     }
   } else if constexpr (LW != 0) {
     // Step j: after the barrier block j is in slot j % SV.
-    for (int64_t j0 = 0; j0 < steps; j0 += SV) {
+    for (int j0 = 0; j0 < steps; j0 += SV) {
 #pragma unroll
       for (int u = 0; u < SV; u++) {
-        const int64_t j = j0 + u;
+        const int j = j0 + u;
         if (j >= steps) break;
         asm volatile("s_barrier" ::: "memory");
         if (j < nit) compute(kr[0], kr[0].m, u, wave + kWaves * j);
@@ -822,10 +813,10 @@ __global__ void __launch_bounds__(kThreads + 64 * LW) sdpa_mfma_kernel(SdpaArgs 
     for (int u = 0; u < SV - 1; u++) ld.vload(u, arr(u) + wslot);
 #pragma unroll
     for (int u = 0; u < PK; u++) ld.kload(u, kr[u]);
-    for (int64_t i0 = 0; i0 < nit; i0 += U) {
+    for (int i0 = 0; i0 < nit; i0 += U) {
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        const int64_t i = i0 + u;
+        const int i = i0 + u;
         if constexpr (MK == 2) ld.mload(i, mcur.m);
         ld.kload(i + PK, kr[(u + PK) % (PK + 1)]);
         ld.vload(i + SV - 1, arr((u + SV - 1) % SV) + wslot);
