@@ -258,6 +258,87 @@ def test_prefill_rows_shape_is_invariant_and_accurate(cuda, dname, dtype, D):
 
 
 @pytest.mark.parametrize("dname,dtype", LOW + [("float32", torch.float32)])
+def test_base_moves_in_later_blocks_for_some_columns(cuda, dname, dtype):
+    """Scores that rise along the keys for some (row, head) columns and stay
+    flat for others: head dim 0 carries k_i[0] = i / 2 and q[0] = a slope of
+    0, 0.5, 1 or 1.5 by (row + head) mod 4, so a chain's lazily moved base
+    (reference _attention.py:99-114, the online softmax) moves again in later
+    blocks for some columns of a wave or workgroup (every block of a chain at
+    the steeper slopes, every other block at 0.5) and never after the first
+    for the flat ones. A block whose base moves for some columns takes the
+    full step for the whole wave, where the others keep m and f = 1. Every
+    launch shape gives the same bits, without a mask and end-aligned causal,
+    and rows 0, 31 and 63 are no worse than 4x the reference-order fp32
+    restatement against float64, and within the float64 bound (bf16, f16;
+    fp32 within 2e-5: on these scores the restatement itself exceeds the
+    random-input bound of 2e-6)."""
+    B, H, Hkv, qL, N, D = 1, 8, 2, 64, 640, 128
+    q = rn((B, H, qL, D), torch.float32, 121, std=0.3)
+    k = rn((B, Hkv, N, D), torch.float32, 122, std=0.3)
+    v = rn((B, Hkv, N, D), dtype, 123, device=cuda)
+    slope = ((torch.arange(qL).view(1, 1, qL) + torch.arange(H).view(1, H, 1)) % 4) * 0.5
+    q[..., 0] = slope.to(torch.float32)
+    k[..., 0] = torch.arange(N, dtype=torch.float32).view(1, 1, N) / 2
+    q, k = q.to(dtype).to(cuda), k.to(dtype).to(cuda)
+    shapes = shapes_for(dtype, D, D, H // Hkv)
+    assert len(shapes) >= (2 if dtype == torch.float32 else 5), shapes
+    rows = [0, 31, 63]
+    for label, spec in (("none", None), ("end", "end")):
+        ref = None
+        for sh in shapes:
+            y = run(q, k, v, spec, shape=sh)
+            case = "%s %s shape %d" % (dname, label, sh)
+            assert torch.isfinite(y).all(), case
+            if ref is None:
+                ref = bits(y)
+                ours = f64(y[0:1, :, rows])
+                want, fixed = _oracle_rows(q, k, v, spec, rows, 0, dname)
+                scale = max(np.abs(want).max(), 1e-30)
+                err = np.abs(ours - want).max() / scale
+                err_fixed = np.abs(fixed - want).max() / scale
+                # fp32: scores in the hundreds, rescaled block after block,
+                # take the reference-order restatement past the random-input
+                # bound too; the restatement ratio is the check there.
+                tol = 2e-5 if dtype == torch.float32 else TOL[dname]
+                assert err < tol, "%s: %.3e (restatement %.3e)" % (case, err, err_fixed)
+                assert err < 4 * err_fixed + 1e-7, "%s: %.3e vs %.3e" % (case, err, err_fixed)
+            else:
+                d = int((bits(y) != ref).sum())
+                assert d == 0, "%s: %d differ" % (case, d)
+
+
+def test_key_value_views_spanning_more_than_4_gib(cuda):
+    """Key and value views whose rows are 1 MiB apart (the first 128 elements
+    of each row of a wider cache), so that from a block's first row to the
+    last visible row spans more than 4 GiB: the kernels' per-block buffer
+    resources cap their byte count at 2^31 - 1 (a block's own rows lie within
+    32 rows). Every bf16 launch shape gives, at decode and at a causal prefill
+    chunk, the bits of the same call on compact copies."""
+    dtype = torch.bfloat16
+    B, H, Hkv, N, D, RS = 1, 8, 1, 4352, 128, 1 << 19
+    assert (N - 1) * RS * 2 > 1 << 32
+    kc = rn((B, Hkv, N, D), dtype, 131, device=cuda)
+    vc = rn((B, Hkv, N, D), dtype, 132, device=cuda)
+    kw = torch.zeros(N, RS, dtype=dtype, device=cuda)
+    vw = torch.zeros(N, RS, dtype=dtype, device=cuda)
+    kw[:, :D] = kc[0, 0]
+    vw[:, :D] = vc[0, 0]
+    kv, vv = kw[:, :D][None, None], vw[:, :D][None, None]
+    assert kv.shape == (B, Hkv, N, D) and kv.stride()[2:] == (RS, 1)
+    try:
+        for qL, spec in ((1, None), (64, "end")):
+            q = rn((B, H, qL, D), dtype, 133 + qL, device=cuda)
+            for sh in [None] + shapes_for(dtype, D, D, H // Hkv):
+                case = (qL, spec, sh)
+                got, want = run(q, kv, vv, spec, shape=sh), run(q, kc, vc, spec, shape=sh)
+                assert torch.isfinite(got).all(), case
+                assert np.array_equal(bits(got), bits(want)), case
+    finally:
+        del kw, vw, kv, vv
+        torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dname,dtype", LOW + [("float32", torch.float32)])
 def test_unwritten_cache_tail_never_reaches_the_output(cuda, dname, dtype):
     """Keys past every row's causal horizon hold NaN (an unwritten cache tail):
     the output is finite and bitwise equal to the same call with a zero tail,
