@@ -955,56 +955,50 @@ struct Shared {
   // rather than lambdas in the kernel: a lambda there that makes buffer
   // resources cost the kernel its host stub.)
   struct Loads {
-    const T* kb;
-    const T* vb;
-    // The next block's first key and value rows, the bytes from there to
-    // the end of the last row some column sees, 32 rows in bytes, and the
-    // blocks left to load (issue() walks the blocks in order).
-    const char* kp;
-    const char* vp;
-    int64_t krem, vrem, kstep, vstep;
+    // A wave's loads all fall in one stream, keys or values (the key loads
+    // are a whole number of waves' shares), so it keeps one stream's state:
+    // the next block's first row, the bytes from there to the end of the
+    // last row some column sees, 32 rows in bytes, and the blocks left to
+    // load (issue() walks the blocks in order).
+    static_assert((KSLOT / 64) % LPW == 0, "a wave's loads lie in one stream");
+    const char* sp;
+    int64_t srem, sstep;
     int left;
     uint32_t loff[LPW];
-    bool lkey[LPW];
     __device__ __forceinline__ void init(const SdpaArgs& p, int64_t b, int64_t kvh, int64_t kmax,
                                          int nblk, int wave, int lane) {
       constexpr uint32_t E = sizeof(T);
-      const int64_t ks2 = p.ks[2], vs2 = p.vs[2];
-      kp = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1]);
-      vp = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1]);
-      krem = ((kmax - 1) * ks2 + D) * E;
-      vrem = ((kmax - 1) * vs2 + V) * E;
-      kstep = kBlk * ks2 * E;
-      vstep = kBlk * vs2 * E;
+      const bool keys = wave * LPW < KSLOT / 64;  // wave-uniform
+      const int64_t s2 = keys ? p.ks[2] : p.vs[2];
+      const T* base = keys ? static_cast<const T*>(p.k) + b * p.ks[0] + kvh * p.ks[1]
+                           : static_cast<const T*>(p.v) + b * p.vs[0] + kvh * p.vs[1];
+      sp = reinterpret_cast<const char*>(base);
+      srem = ((kmax - 1) * s2 + (keys ? D : V)) * E;
+      sstep = kBlk * s2 * E;
       left = nblk;
 #pragma unroll
       for (int u = 0; u < LPW; u++) {
         const int j = wave * LPW + u;
-        lkey[u] = j < KSLOT / 64;
-        if (lkey[u]) {
+        if (keys) {
           const int pos = j * 64 + lane, r = pos / CH, c = (pos % CH) ^ swz_k(r);
-          loff[u] = (uint32_t)((r * ks2 + c * 8) * E);
+          loff[u] = (uint32_t)((r * s2 + c * 8) * E);
         } else {
           const int pos = (j - KSLOT / 64) * 64 + lane, r = pos / VCH, c = vchunk_src(r, pos % VCH);
-          loff[u] = (uint32_t)((r * vs2 + c * 8) * E);
+          loff[u] = (uint32_t)((r * s2 + c * 8) * E);
         }
       }
     }
     // This wave's loads of the next block into the slot at dst (the slot's
     // first uint4 plus this wave's first load). While blocks are left, the
-    // remaining byte counts are at least one row (D or V elements).
+    // remaining byte count is at least one row (D or V elements).
     __device__ __forceinline__ void issue(uint4* dst) {
-      const bool in = left > 0;
-      const auto rk = make_rsrc_n(kp, in ? clamp31(krem) : 0u);
-      const auto rv = make_rsrc_n(vp, in ? clamp31(vrem) : 0u);
+      const auto rs = make_rsrc_n(sp, left > 0 ? clamp31(srem) : 0u);
 #pragma unroll
       for (int u = 0; u < LPW; u++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(lkey[u] ? rk : rv, (lds_void_t*)(dst + u * 64),
-                                                 16, (int)loff[u], 0, 0, 0);
-      kp += kstep;
-      vp += vstep;
-      krem -= kstep;
-      vrem -= vstep;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(dst + u * 64), 16, (int)loff[u],
+                                                 0, 0, 0);
+      sp += sstep;
+      srem -= sstep;
       left--;
     }
   };
