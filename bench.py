@@ -408,6 +408,10 @@ def main():
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--feed-probe", action="store_true",
                     help="only run the per-CU operand feed probe (bi_feed_probe) and print it")
+    ap.add_argument("--quantized", action="store_true",
+                    help="only run the 4-bit quantized linear (4096x4096, group 64) and the "
+                         "dense bi.linear on the same shape, at 1 and 256 rows, five launches "
+                         "each (for counter passes)")
     ap.add_argument("--prefill-shape", choices=("rows", "shared"),
                     help="only run the causal prefill (B=1, 32/8 heads, L=2048, D=128, bf16) "
                          "five times through one forced attention launch shape (for counter "
@@ -437,6 +441,21 @@ def main():
         return
     if args.feed_probe:
         print(json.dumps({"feed_probe": feed_probe(torch, dev)}))
+        return
+    if args.quantized:
+        g = torch.Generator().manual_seed(0)
+        wq = (torch.randn(4096, 4096, generator=g) / 64).to(torch.bfloat16)
+        qw, qs, qz = (t.to(dev) for t in bi.quantize(wq, 64, 4))
+        wd = wq.to(dev)
+        for Mq in (1, 256):
+            xq = torch.randn(Mq, 4096, generator=g).to(torch.bfloat16).to(dev)
+            for _ in range(5):
+                bi.quantized_linear(xq, qw, qs, qz, 64, 4)
+            for _ in range(5):
+                bi.linear(xq, wd)
+        torch.cuda.synchronize()
+        print(json.dumps({"quantized": "4-bit g64 4096x4096 and dense bf16, M in (1, 256)",
+                          "launches": 5}))
         return
     if args.prefill_shape:
         from mlx_batch_invariant import _attention, _lib
