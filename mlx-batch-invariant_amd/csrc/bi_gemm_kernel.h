@@ -1418,8 +1418,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
 // Footprints of C per workgroup. Every entry runs the same per-element
 // arithmetic; the table only trades parallelism against operand reuse and
 // latency hiding. Columns: id, BM, BN, WM, WN, NW (waves), KB (stage bytes),
-// NS (LDS ring stages), PL (loading waves issue all loads), PP (ping-pong
-// schedule of the compute waves).
+// NS (LDS ring stages), PL (loading waves issue all loads), PP (1: ping-pong
+// schedule of the compute waves; 2: the four-wave footprint of bi_gemm_w4.h,
+// whose KB and NS describe its stage and its ring of 32 KB slots).
 #define BI_GEOMETRIES(X)                     \
   X(0, 16, 16, 1, 1, 4, 512, 4, 0, 0)        \
   X(1, 64, 16, 4, 1, 4, 256, 4, 0, 0)        \
@@ -1427,9 +1428,16 @@ __global__ void __launch_bounds__(64 * NW) gemm_qkernel(GemmArgs p) {
   X(3, 128, 128, 4, 2, 8, 128, 4, 0, 0)      \
   X(4, 256, 128, 4, 2, 12, 128, 3, 1, 0)     \
   X(5, 64, 32, 4, 2, 8, 256, 3, 0, 0)        \
-  X(6, 256, 256, 4, 4, 16, 64, 4, 0, 1)
+  X(6, 256, 256, 4, 4, 16, 64, 4, 0, 1)      \
+  X(7, 256, 256, 2, 2, 4, 128, 5, 0, 2)
 
 using KernelFn = void (*)(GemmArgs);
+
+}  // namespace bi_gemm_dev
+
+#include "bi_gemm_w4.h"
+
+namespace bi_gemm_dev {
 
 // Kernel for geometry g in the translation unit of element type T.
 template <typename T>
@@ -1438,9 +1446,17 @@ KernelFn kernel_for(int g, bool trans_b) {
 // (at most 168 registers each) the 64 x 64 wave tiles do not fit.
 #define BI_GEO_CASE(id, bm, bn, wm, wn, nw, kb, ns, pl, pp)                             \
   case id:                                                                             \
-    if constexpr (sizeof(T) == 4 && (nw > 8 || pp)) return nullptr;                    \
-    else return trans_b ? gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, pl, pp>     \
-                        : gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, false, pl, pp>;
+    if constexpr (pp == 2) {                                                           \
+      if constexpr (sizeof(T) == 2)                                                    \
+        return trans_b ? gemm_w4_kernel<T, true> : gemm_w4_kernel<T, false>;           \
+      else                                                                             \
+        return nullptr;                                                                \
+    } else if constexpr (sizeof(T) == 4 && (nw > 8 || pp)) {                           \
+      return nullptr;                                                                  \
+    } else {                                                                           \
+      return trans_b ? gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, true, pl, pp != 0>   \
+                     : gemm_kernel<T, bm, bn, wm, wn, nw, kb, ns, false, pl, pp != 0>; \
+    }
   switch (g) { BI_GEOMETRIES(BI_GEO_CASE) }
 #undef BI_GEO_CASE
   return nullptr;

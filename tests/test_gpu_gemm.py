@@ -137,11 +137,12 @@ def test_all_geometries_agree(cuda, trans_b):
 @pytest.mark.parametrize("trans_b", [False, True])
 def test_large_footprints_agree(cuda, trans_b):
     """The large-M footprints (128 x 128, 256 x 128 with loading waves, 256 x
-    256 ping-pong) over several rounds of workgroups, with ragged M, N and K
-    tails and a partial group of row blocks, give the same bits; at M = 4096
-    bi_gemm picks 256 x 256 and a row keeps its M = 1 bits there."""
+    256 ping-pong, 256 x 256 with four waves) over several rounds of
+    workgroups, with ragged M, N and K tails and a partial group of row
+    blocks, give the same bits; at M = 4096 bi_gemm picks a 256 x 256
+    footprint and a row keeps its M = 1 bits there."""
     geos = _gemm.geometries()
-    big = [geos.index(f) for f in ((128, 128, 8), (256, 128, 12), (256, 256, 16))]
+    big = [geos.index(f) for f in ((128, 128, 8), (256, 128, 12), (256, 256, 16), (256, 256, 4))]
     for dname, dtype in DTYPES[1:]:
         M, K, N = 4360, 1032, 4104
         a = rn((M, K), dtype, 41, device=cuda)
@@ -156,7 +157,8 @@ def test_large_footprints_agree(cuda, trans_b):
         b = rn((N, K) if trans_b else (K, N), dtype, 45, std=K ** -0.5, device=cuda)
         from mlx_batch_invariant import _lib
         assert geos[_lib.lib().bi_gemm_pick_geometry(M, N, K, _lib.DTYPE_CODES[dtype],
-                                                     int(trans_b))] == (256, 256, 16)
+                                                     int(trans_b))] == (
+            (256, 256, 4) if trans_b else (256, 256, 16))
         y = bits(_gemm._gemm(a, b, None, trans_b)).reshape(M, N)
         for r in (0, 1, 2047, 4095):
             one = bits(_gemm._gemm(a[r:r + 1].contiguous(), b, None, trans_b))

@@ -76,11 +76,15 @@ def test_footprint_policy():
     # (M = 384), 258 need two, where 516 of 128 x 128 need three (M = 768).
     assert pick(384, 11008) == (256, 128, 12)
     assert pick(512, 11008) == (256, 128, 12)
-    # The 256 x 256 ping-pong footprint once its tiles fill most CUs.
-    assert pick(768, 11008) == (256, 256, 16)
+    # 256 x 256 once its tiles fill most CUs: the four-wave footprint on
+    # (N, K) weights, the 16-wave ping-pong one on (K, N) weights.
+    assert pick(768, 11008) == (256, 256, 4)
+    assert pick(768, 11008, trans_b=0) == (256, 256, 16)
     assert pick(2048, 4096) == (256, 128, 12)                   # 128 tiles of 256 x 256
     assert pick(1024, 4096) == (128, 128, 8)
-    assert pick(4096, 4096) == pick(4096, 11008) == pick(1024, 32000) == (256, 256, 16)
+    assert pick(4096, 4096) == pick(4096, 11008) == pick(1024, 32000) == (256, 256, 4)
+    assert (pick(4096, 4096, trans_b=0) == pick(4096, 11008, trans_b=0)
+            == pick(1024, 32000, trans_b=0) == (256, 256, 16))
     assert pick(256, 512) == (64, 16, 4)                        # small output
     assert pick(256, 4096) == (64, 64, 8)
     assert pick(256, 11008) == (128, 128, 8)
