@@ -62,6 +62,13 @@ int bi_gemm_timed(const void* a, const void* b, const void* bias, void* out, int
 int bi_feed_probe(const void* src, int64_t panel_bytes, int panels, int stages, int workgroups,
                   void* start_event, void* stop_event, void* hip_stream);
 
+/* Number of geometries bi_qgemm_with_geometry accepts: the GEMM geometries
+ * (bi_gemm_num_geometries()), then the quantized decode footprint, id
+ * bi_gemm_num_geometries(): 16 output columns per workgroup whose waves split
+ * K by groups (4-bit weights and at most 4 rows of x only; otherwise
+ * BI_EUNSUPPORTED). No counterpart in the reference. */
+int bi_qgemm_num_geometries(void);
+
 /* bi_qgemm with the geometry forced to `g` (same arguments and semantics). */
 int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
                            const void* biases, void* out, int64_t M, int64_t N, int64_t K,

@@ -135,7 +135,12 @@ int pick_geometry(int64_t M, int64_t N, int dtype, int trans_b) {
 // dense rules, except that 128 x 128 must fill the CUs (its workgroups
 // dequantize twice the columns: N = 11008, M = 256: 64 x 64 61 us, 128 x 128
 // 70 us).
-int pick_qgeometry(int64_t M, int64_t N) {
+// Id of the quantized decode footprint (bi_gemm_qdecode.h: 4-bit codes, at
+// most 4 rows), one past the dense table.
+constexpr int kQDecode = kNumGeometries;
+
+int pick_qgeometry(int64_t M, int64_t N, int bits) {
+  if (M <= 4 && bits == 4) return kQDecode;
   if (M <= 16) return 0;
   const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);
   const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
@@ -392,9 +397,43 @@ int qvalidate(const void* x, const void* w, const void* scales, const void* bias
   return BI_OK;
 }
 
+// The decode footprint: one workgroup per 16 output columns.
+int qlaunch_decode(const void* x, const void* w, const void* scales, const void* biases,
+                   void* out, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                   int dtype, void* stream) {
+  if (bits != 4 || M > 4)
+    return bi::fail(BI_EUNSUPPORTED,
+                    "bi_qgemm: the decode footprint takes 4-bit weights and at most 4 rows");
+  const int64_t lim = (int64_t)1 << 31;
+  if (M * K * 2 >= lim || 16 * K / 2 >= lim)
+    return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: operand panel of 2 GiB or more");
+  GemmArgs p = {};
+  p.a = x;
+  p.b = w;
+  p.out = out;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.qs = scales;
+  p.qz = biases;
+  p.qgroup_shift = group_shift(group_size);
+  const int64_t blocks = ceil_div(N, 16);
+  if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_qgemm: too many tiles");
+  KernelFn fn = dtype == BI_F16 ? bi_qdecode_kernel_f16(group_size, (int)M)
+                                : bi_qdecode_kernel_bf16(group_size, (int)M);
+  if (!fn) return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: decode footprint not built");
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * bi_gemm_dev::kQDecodeWaves),
+                     0, static_cast<hipStream_t>(stream), p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return bi::launch_error(e, "bi_qgemm launch");
+  return BI_OK;
+}
+
 int qlaunch(const void* x, const void* w, const void* scales, const void* biases, void* out,
             int64_t M, int64_t N, int64_t K, int group_size, int bits, int dtype, int g,
             void* stream) {
+  if (g == kQDecode)
+    return qlaunch_decode(x, w, scales, biases, out, M, N, K, group_size, bits, dtype, stream);
   const Geometry& G = kGeometries[g];
   const int64_t lim = (int64_t)1 << 31;
   if ((int64_t)G.bm * K * 2 >= lim || (int64_t)G.bn * K * bits / 8 >= lim)
@@ -435,14 +474,16 @@ extern "C" int bi_qgemm(const void* x, const void* w, const void* scales, const 
   const int rc = qvalidate(x, w, scales, biases, out, M, N, K, group_size, bits, dtype);
   if (rc != BI_OK || M == 0 || N == 0) return rc;
   return qlaunch(x, w, scales, biases, out, M, N, K, group_size, bits, dtype,
-                 pick_qgeometry(M, N), hip_stream);
+                 pick_qgeometry(M, N, bits), hip_stream);
 }
+
+extern "C" int bi_qgemm_num_geometries(void) { return kQDecode + 1; }
 
 extern "C" int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
                                       const void* biases, void* out, int64_t M, int64_t N,
                                       int64_t K, int group_size, int bits, int dtype, int g,
                                       void* hip_stream) {
-  if (g < 0 || g >= kNumGeometries) return bi::fail(BI_EINVAL, "unknown geometry %d", g);
+  if (g < 0 || g > kQDecode) return bi::fail(BI_EINVAL, "unknown geometry %d", g);
   const int rc = qvalidate(x, w, scales, biases, out, M, N, K, group_size, bits, dtype);
   if (rc != BI_OK || M == 0 || N == 0) return rc;
   return qlaunch(x, w, scales, biases, out, M, N, K, group_size, bits, dtype, g, hip_stream);

@@ -1436,6 +1436,7 @@ using KernelFn = void (*)(GemmArgs);
 }  // namespace bi_gemm_dev
 
 #include "bi_gemm_w4.h"
+#include "bi_gemm_qdecode.h"
 
 namespace bi_gemm_dev {
 
@@ -1493,6 +1494,26 @@ KernelFn qkernel_for(int g, int bits, int group) {
   return nullptr;
 }
 
+// The quantized decode footprint (4-bit codes, at most 4 rows) for group size
+// `group` and `rows` rows of x, kQDecodeWaves waves per workgroup.
+constexpr int kQDecodeWaves = 4;
+template <typename T, int GS>
+KernelFn qdecode_kernel_rows(int rows) {
+  constexpr int NW = kQDecodeWaves;
+  if (rows <= 1) return gemm_qdecode_kernel<T, GS, 1, NW>;
+  if (rows == 2) return gemm_qdecode_kernel<T, GS, 2, NW>;
+  return gemm_qdecode_kernel<T, GS, 4, NW>;
+}
+template <typename T>
+KernelFn qdecode_kernel_for(int group, int rows) {
+  switch (group) {
+    case 32: return qdecode_kernel_rows<T, 32>(rows);
+    case 64: return qdecode_kernel_rows<T, 64>(rows);
+    case 128: return qdecode_kernel_rows<T, 128>(rows);
+  }
+  return nullptr;
+}
+
 }  // namespace bi_gemm_dev
 
 // Per-type kernel tables, defined in bi_gemm_{f32,f16,bf16}.hip.
@@ -1501,3 +1522,5 @@ bi_gemm_dev::KernelFn bi_gemm_kernel_f16(int g, bool trans_b);
 bi_gemm_dev::KernelFn bi_gemm_kernel_bf16(int g, bool trans_b);
 bi_gemm_dev::KernelFn bi_qgemm_kernel_f16(int g, int bits, int group);
 bi_gemm_dev::KernelFn bi_qgemm_kernel_bf16(int g, int bits, int group);
+bi_gemm_dev::KernelFn bi_qdecode_kernel_f16(int group, int rows);
+bi_gemm_dev::KernelFn bi_qdecode_kernel_bf16(int group, int rows);

@@ -1,0 +1,311 @@
+// The quantized decode footprint of the batch-invariant GEMM: 4-bit affine
+// weights, 16-bit activations, at most 4 rows of x. Included by
+// bi_gemm_kernel.h; every element runs the quantized sequence of that file's
+// quantized section: per group of K, P = the group's chunk-steps (ascending,
+// the first from +0.0) of v_mfma_f32_16x16x32_{bf16,f16} on the x chunk and
+// the codes as element-type integers, X the same on a chunk of ones; then, per
+// group in ascending order, acc = fma(scale, P, acc) and acc = fma(bias, X,
+// acc); one rounding at the end.
+//
+// Shape. A workgroup owns 16 output columns (every row: M <= MR <= 4) and NW
+// waves. Groups are independent until their folds, so the waves split K
+// instead of the columns: in a round of RK elements of K, wave w computes P
+// and X of the groups in its BPW consecutive 128-element blocks and leaves
+// them in LDS; after a barrier wave 0 folds the round's groups in ascending
+// order, one output element per lane (lane 16 e + n: row e, column n), and
+// carries acc into the next round.
+//
+// Feed. All of a round's loads are issued at its start, in the order x,
+// codes, scales and biases, so each wait lets the later loads stay in
+// flight: a wave works on its first block of codes while the others land.
+// x (rows 0 .. M - 1 of the round's K range) goes through registers into
+// LDS, rows padded by 64 bytes so the rows' operand reads fall on distinct
+// banks. Lane (g, n) of a wave reads the 16 bytes of block b's codes of
+// weight row n that hold chunk-step 4 b + g's four 32-bit words, one per
+// lane group; a 4 x 4 transpose across the lane groups (two rounds of
+// v_permlane32_swap / v_permlane16_swap) leaves in register j of lane group g
+// its word of chunk-step 4 b + j -- the 8 codes of k = 32 q + 8 g + t, t =
+// 0..7, the MFMA's B operand layout -- so every code load is a whole 16 bytes
+// and no code passes through LDS.
+#pragma once
+
+namespace bi_gemm_dev {
+
+// 4 x 4 transpose of words across the lane groups g = lane / 16: afterwards
+// register j of lane group g holds what register g of lane group j held.
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with
+// the lower 32 of its second; v_permlane16_swap the odd 16-lane rows of its
+// first operand with the even rows of its second.
+__device__ __forceinline__ void xpose_lane_groups(uint32_t (&r)[4]) {
+  const auto s0 = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
+  const auto s1 = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
+  const auto t0 = __builtin_amdgcn_permlane16_swap(s0[0], s1[0], false, false);
+  const auto t1 = __builtin_amdgcn_permlane16_swap(s0[1], s1[1], false, false);
+  r[0] = t0[0];
+  r[1] = t0[1];
+  r[2] = t1[0];
+  r[3] = t1[1];
+}
+
+// The 8 4-bit codes of word w (code t in bits 4t .. 4t + 3) as element-type
+// integers, two per register, code 0 in the low half of the first. Codes 0-15
+// in the low bits of a byte are the fp8 E4M3 values q * 2^-9 (subnormal for
+// q < 8, then the first binade), so the scaled fp8 conversion with scale
+// 2^9 yields q exactly, two codes per instruction: two byte permutes put
+// codes 0-3 and 4-7 one per byte (each byte masked to its low nibble), and
+// four conversions each take one 16-bit half.
+template <typename T>
+__device__ __forceinline__ uint4 codes_as_elems(uint32_t w) {
+  const uint32_t v = w >> 4;
+  const uint32_t lo = __builtin_amdgcn_perm(v, w, 0x05010400u) & 0x0F0F0F0Fu;  // codes 0 1 2 3
+  const uint32_t hi = __builtin_amdgcn_perm(v, w, 0x07030602u) & 0x0F0F0F0Fu;  // codes 4 5 6 7
+  uint4 r;
+  if constexpr (IsBF16<T>::value) {
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, true));
+  } else {
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true));
+  }
+  return r;
+}
+
+template <int GS, int MR, int NW>
+struct QDecode {
+  static constexpr int RK = 4096;             // elements of K per round
+  static constexpr int RG = RK / GS;          // groups per round
+  static constexpr int CPG = GS / 32;         // chunk-steps per group
+  static constexpr int NT = 64 * NW;
+  static constexpr int BPW = RK / 128 / NW;   // blocks of 128 elements per wave per round
+  static constexpr int XROW = RK * 2 + 64;    // bytes per staged row of x
+  static constexpr int XPL = RK / 8 / NT;     // 16-byte x chunks per thread and row
+  static constexpr int SRS = RG + 4;          // scale/bias row stride (f32), banks apart
+  static constexpr int SPL = 16 * RG / NT;    // scale (and bias) entries per thread
+  static_assert((RK / 8) % NT == 0 && (16 * RG) % NT == 0 && BPW >= 1, "round split");
+  static_assert(GS >= 32 && GS <= 128, "groups of one to four chunk-steps: a block holds whole groups");
+  static_assert(MR >= 1 && MR <= 4, "one to four rows");
+  // LDS: x rows; P of each group (rows 0 .. MR - 1, 16 columns, [row][column]);
+  // X of each group (rows 0 .. MR - 1); scales and biases as fp32, a row per
+  // column; and 256 bytes that lanes with nothing to store write to instead
+  // (so the stores need no branch; nothing reads them).
+  static constexpr int OFF_P = MR * XROW;
+  static constexpr int OFF_X = OFF_P + RG * MR * 64;
+  static constexpr int OFF_S = OFF_X + RG * 16;
+  static constexpr int OFF_Z = OFF_S + 16 * SRS * 4;
+  static constexpr int OFF_DUMMY = OFF_Z + 16 * SRS * 4;
+  static constexpr int LDS_BYTES = OFF_DUMMY + 256;
+};
+
+template <typename T, int GS, int MR, int NW>
+__global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
+  using D = QDecode<GS, MR, NW>;
+  constexpr int RK = D::RK, RG = D::RG, CPG = D::CPG, BPW = D::BPW, NT = D::NT;
+  constexpr int64_t E = 2;
+  __shared__ __attribute__((aligned(16))) char lds[D::LDS_BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r16 = lane & 15;
+  const int64_t M = p.M, N = p.N, K = p.K;
+  const int mrows = (int)M;  // 1 .. MR (the host checks)
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t G = K / GS;         // groups
+  const int64_t nq = K / 32;        // chunk-steps
+  const int64_t qrow = K / 2;       // bytes of packed codes per weight row
+  const int64_t cols = min((int64_t)16, N - n0);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.a, M * K * E);
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(static_cast<const char*>(p.b) + n0 * qrow, cols * qrow);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(static_cast<const T*>(p.qs) + n0 * G, cols * G * E);
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(static_cast<const T*>(p.qz) + n0 * G, cols * G * E);
+
+  // The A operand of chunk-step q of the round: lane (g, r) reads x row r at
+  // k = 32 q + 8 g from the staged rows; rows past M read row 0 (an output
+  // row depends only on its own row of x, and rows past M are not written).
+  const uint32_t a_base = (uint32_t)((r16 < mrows ? r16 : 0) * D::XROW + 16 * g);
+  constexpr uint32_t ONE = IsBF16<T>::value ? 0x3F803F80u : 0x3C003C00u;
+  const uint4 ones = make_uint4(ONE, ONE, ONE, ONE);
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+
+  float acc = 0.f;  // wave 0: element (row lane / 16, column lane % 16)
+  const int64_t rounds = (K + RK - 1) / RK;
+  for (int64_t rr = 0; rr < rounds; rr++) {
+    // The round index passes through an empty asm statement: nothing below
+    // is then invariant across rounds, so the compiler hoists no address
+    // arithmetic out of the loop (it would hold registers in every phase).
+    int32_t r32 = (int32_t)rr;
+    asm volatile("" : "+s"(r32));
+    const int64_t r = r32;
+    const int64_t k0 = r * RK;
+    // Loads: x chunks of rows 0 .. M - 1 (the row of chunk i is the same for
+    // every thread), this wave's blocks of codes, scale and bias entries.
+    uint4 xv[MR][D::XPL];
+#pragma unroll
+    for (int row = 0; row < MR; row++)
+#pragma unroll
+      for (int i = 0; i < D::XPL; i++) {
+        const int kc = tid + i * NT;
+        const int64_t k = k0 + kc * 8;
+        if (row < mrows) xv[row][i] = buffer_chunk(rx, k < K ? (uint32_t)((row * K + k) * E) : kOutOfRange);
+      }
+    uint32_t cw[BPW][4];
+#pragma unroll
+    for (int j = 0; j < BPW; j++) {
+      const int64_t q = (k0 >> 5) + 4 * (wave * BPW + j) + g;  // chunk-step this lane's 16 bytes hold
+      const uint32_t off = q < nq ? (uint32_t)(r16 * qrow + q * 16) : kOutOfRange;
+      const uint4 v = buffer_chunk(rw, off);
+      cw[j][0] = v.x;
+      cw[j][1] = v.y;
+      cw[j][2] = v.z;
+      cw[j][3] = v.w;
+    }
+    unsigned short sv[D::SPL], zv[D::SPL];
+#pragma unroll
+    for (int i = 0; i < D::SPL; i++) {
+      const int e = tid + i * NT, col = e / RG, gi = e % RG;
+      const int64_t grp = r * RG + gi;
+      const uint32_t off = grp < G ? (uint32_t)((col * G + grp) * E) : kOutOfRange;
+      sv[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0);
+      zv[i] = __builtin_amdgcn_raw_buffer_load_b16(rz, (int)off, 0, 0);
+    }
+#pragma unroll
+    for (int row = 0; row < MR; row++)
+#pragma unroll
+      for (int i = 0; i < D::XPL; i++) {
+        const int kc = tid + i * NT;
+        if (row < mrows) *reinterpret_cast<uint4*>(lds + row * D::XROW + kc * 16) = xv[row][i];
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // This wave's groups: P and X of each into LDS. The x operands of a
+    // block are read while the previous block computes; when all of the
+    // wave's blocks lie inside K (FULL) the blocks run without bound tests.
+    // Lane group 0 stores P (rows 0 .. MR - 1 of its column), lane 0 stores
+    // X; every other lane stores into its own 4 bytes of the dummy area. (The
+    // masks pass through an empty asm statement so that each store address is
+    // computed where it is used.)
+    const int64_t q0 = k0 >> 5;              // the round's first chunk-step
+    const int64_t qw = q0 + 4 * wave * BPW;  // this wave's first chunk-step
+    uint32_t p_at = g == 0 ? (uint32_t)(D::OFF_P + r16 * 4) : (uint32_t)(D::OFF_DUMMY + lane * 4);
+    uint32_t p_gmask = g == 0 ? ~0u : 0u;
+    uint32_t x_at = lane == 0 ? (uint32_t)D::OFF_X : (uint32_t)(D::OFF_DUMMY + lane * 4);
+    uint32_t x_gmask = lane == 0 ? ~0u : 0u;
+    asm volatile("" : "+v"(p_gmask), "+v"(x_gmask), "+v"(p_at), "+v"(x_at));
+    const auto blocks = [&](auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      uint4 av[2][4];
+      const auto read_x = [&](int j, uint4 (&dst)[4]) {
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+          dst[jj] = *reinterpret_cast<const uint4*>(lds + a_base + 64 * (uint32_t)(qw + 4 * j + jj - q0));
+      };
+      read_x(0, av[0]);
+#pragma unroll
+      for (int j = 0; j < BPW; j++) {
+        const int64_t qb = qw + 4 * j;
+        if (!FULL && qb >= nq) break;
+        if (j + 1 < BPW) read_x(j + 1, av[(j + 1) & 1]);
+        xpose_lane_groups(cw[j]);
+        f32x4_t P = zero, X = zero;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const int64_t q = qb + jj;
+          if (!FULL && q >= nq) break;
+          const uint4 bv = codes_as_elems<T>(cw[j][jj]);
+          const bool first = (jj % CPG) == 0;  // blocks start on group boundaries
+          P = chunk_step(T(0), av[j & 1][jj], bv, first ? zero : P);
+          X = chunk_step(T(0), av[j & 1][jj], ones, first ? zero : X);
+          if ((jj % CPG) == CPG - 1) {
+            const uint32_t gi = (uint32_t)((q - q0) / CPG);
+#pragma unroll
+            for (int e = 0; e < MR; e++) {
+              *reinterpret_cast<float*>(lds + p_at + ((gi * (MR * 64) + e * 64) & p_gmask)) = P[e];
+              *reinterpret_cast<float*>(lds + x_at + ((gi * 16 + e * 4) & x_gmask)) = X[e];
+            }
+          }
+        }
+        // Keeps the scheduler from hoisting later blocks' operand reads.
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    if (qw + 4 * BPW <= nq)
+      blocks(std::true_type{});
+    else
+      blocks(std::false_type{});
+    float* ss = reinterpret_cast<float*>(lds + D::OFF_S);
+    float* zs = reinterpret_cast<float*>(lds + D::OFF_Z);
+#pragma unroll
+    for (int i = 0; i < D::SPL; i++) {
+      const int e = tid + i * NT, col = e / RG, gi = e % RG;
+      ss[col * D::SRS + gi] = Elem<T>::to_f32(__builtin_bit_cast(T, sv[i]));
+      zs[col * D::SRS + gi] = Elem<T>::to_f32(__builtin_bit_cast(T, zv[i]));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    if (wave == 0) {
+      // The round's groups in ascending order, FC at a time, the operands of
+      // the next FC read while these fold.
+      constexpr int FC = 8;
+      const int e = lane >> 4, n = lane & 15;
+      const int ng = (int)min((int64_t)RG, G - r * RG);
+      uint32_t op = D::OFF_P + (e * 16 + n) * 4, ox = D::OFF_X + e * 4, os = n * D::SRS * 4;
+      asm volatile("" : "+v"(op), "+v"(ox), "+v"(os));
+      const float* Pf = reinterpret_cast<const float*>(lds + op);  // group gi: [MR * 16 gi]
+      const float* Xf = reinterpret_cast<const float*>(lds + ox);  // [4 gi]
+      const f32x4_t* Sf = reinterpret_cast<const f32x4_t*>(lds + D::OFF_S + os);
+      const f32x4_t* Zf = reinterpret_cast<const f32x4_t*>(lds + D::OFF_Z + os);
+      struct Ops {
+        float p[FC], x[FC];
+        f32x4_t s[FC / 4], z[FC / 4];
+      };
+      const auto load = [&](int c, Ops& o) {
+#pragma unroll
+        for (int i = 0; i < FC; i++) {
+          o.p[i] = Pf[(c * FC + i) * MR * 16];
+          o.x[i] = Xf[(c * FC + i) * 4];
+        }
+#pragma unroll
+        for (int i = 0; i < FC / 4; i++) {
+          o.s[i] = Sf[c * (FC / 4) + i];
+          o.z[i] = Zf[c * (FC / 4) + i];
+        }
+      };
+      const auto fold = [&](const Ops& o) {
+#pragma unroll
+        for (int i = 0; i < FC; i++) {
+          acc = __builtin_fmaf(o.s[i / 4][i % 4], o.p[i], acc);
+          acc = __builtin_fmaf(o.z[i / 4][i % 4], o.x[i], acc);
+        }
+      };
+      const int nfull = ng / FC;
+      Ops o0, o1;
+      if (nfull > 0) load(0, o0);
+      for (int c = 0; c < nfull; c += 2) {
+        if (c + 1 < nfull) load(c + 1, o1);
+        fold(o0);
+        if (c + 1 < nfull) {
+          if (c + 2 < nfull) load(c + 2, o0);
+          fold(o1);
+        }
+      }
+      const float* Ss = reinterpret_cast<const float*>(Sf);
+      const float* Zs = reinterpret_cast<const float*>(Zf);
+      for (int gi = nfull * FC; gi < ng; gi++) {
+        acc = __builtin_fmaf(Ss[gi], Pf[gi * MR * 16], acc);
+        acc = __builtin_fmaf(Zs[gi], Xf[gi * 4], acc);
+      }
+    }
+    if (rr + 1 < rounds) asm volatile("s_barrier" ::: "memory");
+  }
+
+  if (wave == 0) {
+    const int e = lane >> 4, n = lane & 15;
+    if (e < mrows && n < cols) static_cast<T*>(p.out)[e * N + n0 + n] = Elem<T>::from_f32(acc);
+  }
+}
+
+}  // namespace bi_gemm_dev
