@@ -106,6 +106,49 @@ __device__ inline f32x4_t chunk_step(float, uint4 a, uint4 b, f32x4_t c) {
   return c;
 }
 
+// 4 x 4 transpose of words across the lane groups g = lane / 16: afterwards
+// register j of lane group g holds what register g of lane group j held.
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with
+// the lower 32 of its second; v_permlane16_swap the odd 16-lane rows of its
+// first operand with the even rows of its second.
+__device__ __forceinline__ void xpose_lane_groups(uint32_t (&r)[4]) {
+  const auto s0 = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
+  const auto s1 = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
+  const auto t0 = __builtin_amdgcn_permlane16_swap(s0[0], s1[0], false, false);
+  const auto t1 = __builtin_amdgcn_permlane16_swap(s0[1], s1[1], false, false);
+  r[0] = t0[0];
+  r[1] = t0[1];
+  r[2] = t1[0];
+  r[3] = t1[1];
+}
+
+// The 8 4-bit codes of word w (code t in bits 4t .. 4t + 3) as element-type
+// integers, two per register, code 0 in the low half of the first. Codes 0-15
+// in the low bits of a byte are the fp8 E4M3 values q * 2^-9 (subnormal for
+// q < 8, then the first binade), so the scaled fp8 conversion with scale
+// 2^9 yields q exactly, two codes per instruction: two byte permutes put
+// codes 0-3 and 4-7 one per byte (each byte masked to its low nibble), and
+// four conversions each take one 16-bit half.
+template <typename T>
+__device__ __forceinline__ uint4 codes_as_elems(uint32_t w) {
+  const uint32_t v = w >> 4;
+  const uint32_t lo = __builtin_amdgcn_perm(v, w, 0x05010400u) & 0x0F0F0F0Fu;  // codes 0 1 2 3
+  const uint32_t hi = __builtin_amdgcn_perm(v, w, 0x07030602u) & 0x0F0F0F0Fu;  // codes 4 5 6 7
+  uint4 r;
+  if constexpr (IsBF16<T>::value) {
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, true));
+  } else {
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true));
+  }
+  return r;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
 // Remap so that consecutive logical tiles -- which share operand panels -- run
 // on the same XCD.
@@ -956,6 +999,11 @@ struct GemmTile {
       const int q = qtid + i * QNT;
       if (B_U % QNT == 0 || q < B_U) {
         const int r = q / RCU, c = (q % RCU) * CPT;
+        if constexpr (QB == 4) {
+          // One unit is one chunk: eight codes, two per conversion.
+          sl.b[r * RC + (c ^ swz_k<RC>(r))] = codes_as_elems<T>(st.w[i]);
+          continue;
+        }
         uint32_t d[ND];
         spread_codes(st.w[i], d);
 #pragma unroll
