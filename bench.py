@@ -412,6 +412,10 @@ def main():
                     help="only run the 4-bit quantized linear (4096x4096, group 64) and the "
                          "dense bi.linear on the same shape, at 1 and 256 rows, five launches "
                          "each (for counter passes)")
+    ap.add_argument("--prefill-gemm", action="store_true",
+                    help="only run the four configs[4] prefill GEMMs at M=4096 (bi.linear, "
+                         "(N, K) weights, bf16), six launches each, each followed by a "
+                         "synchronisation (for counter passes)")
     ap.add_argument("--prefill-shape", choices=("rows", "shared"),
                     help="only run the causal prefill (B=1, 32/8 heads, L=2048, D=128, bf16) "
                          "five times through one forced attention launch shape (for counter "
@@ -456,6 +460,18 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"quantized": "4-bit g64 4096x4096 and dense bf16, M in (1, 256)",
                           "launches": 5}))
+        return
+    if args.prefill_gemm:
+        g = torch.Generator().manual_seed(0)
+        for K, N in ((4096, 4096), (4096, 11008), (11008, 4096), (4096, 32000)):
+            xg = torch.randn(4096, K, generator=g).to(torch.bfloat16).to(dev)
+            wg = (torch.randn(N, K, generator=g) * K ** -0.5).to(torch.bfloat16).to(dev)
+            for _ in range(6):
+                bi.linear(xg, wg)
+                torch.cuda.synchronize()
+            del xg, wg
+        print(json.dumps({"prefill_gemm": "M=4096 bi.linear on (K, N) in (4096, 4096), "
+                          "(4096, 11008), (11008, 4096), (4096, 32000)", "launches": 6}))
         return
     if args.prefill_shape:
         from mlx_batch_invariant import _attention, _lib
@@ -710,10 +726,15 @@ def main():
                         + Mq * 4096 * 2)
         q_flops = 2.0 * Mq * 4096 * 4096
         q_roof = min(PEAK_BF16_TFLOPS, q_flops / q_bytes * PEAK_HBM_GBS / 1e3)
+        # Device time as well: 20 calls captured in a HIP graph and replayed
+        # (an eager call at M=1 is bound by the host's per-call cost).
+        q_g = graph_us(torch, lambda: bi.quantized_linear(xq, qw, qs, qz, 64, 4))
         quant["M%d" % Mq] = {"bi_us": round(q_bi, 1), "stock_us": round(q_st, 1),
                              "gbps": round(q_bytes / q_bi / 1e3, 1),
                              "tflops": round(q_flops / q_bi / 1e6, 2),
-                             "frac_of_min_roof": round(q_flops / q_bi / 1e6 / q_roof, 4)}
+                             "frac_of_min_roof": round(q_flops / q_bi / 1e6 / q_roof, 4),
+                             "graph_us": round(q_g, 2),
+                             "graph_frac_of_min_roof": round(q_flops / q_g / 1e6 / q_roof, 4)}
 
     progress("invariance check")
     # Invariance spot check: row 0 of every shape of the sweep across batch
