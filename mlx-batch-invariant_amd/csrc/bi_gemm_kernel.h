@@ -1542,7 +1542,7 @@ KernelFn qkernel_for(int g, int bits, int group) {
   return nullptr;
 }
 
-// The quantized decode footprint (4-bit codes, at most 4 rows) for group size
+// The quantized decode footprint (4-bit codes, at most 8 rows) for group size
 // `group` and `rows` rows of x, kQDecodeWaves waves per workgroup.
 constexpr int kQDecodeWaves = 4;
 template <typename T, int GS>
@@ -1550,7 +1550,8 @@ KernelFn qdecode_kernel_rows(int rows) {
   constexpr int NW = kQDecodeWaves;
   if (rows <= 1) return gemm_qdecode_kernel<T, GS, 1, NW>;
   if (rows == 2) return gemm_qdecode_kernel<T, GS, 2, NW>;
-  return gemm_qdecode_kernel<T, GS, 4, NW>;
+  if (rows <= 4) return gemm_qdecode_kernel<T, GS, 4, NW>;
+  return gemm_qdecode_kernel<T, GS, 8, NW>;
 }
 template <typename T>
 KernelFn qdecode_kernel_for(int group, int rows) {

@@ -1,5 +1,5 @@
 // The quantized decode footprint of the batch-invariant GEMM: 4-bit affine
-// weights, 16-bit activations, at most 4 rows of x. Included by
+// weights, 16-bit activations, at most 8 rows of x. Included by
 // bi_gemm_kernel.h; every element runs the quantized sequence of that file's
 // quantized section: per group of K, P = the group's chunk-steps (ascending,
 // the first from +0.0) of v_mfma_f32_16x16x32_{bf16,f16} on the x chunk and
@@ -7,13 +7,13 @@
 // group in ascending order, acc = fma(scale, P, acc) and acc = fma(bias, X,
 // acc); one rounding at the end.
 //
-// Shape. A workgroup owns 16 output columns (every row: M <= MR <= 4) and NW
+// Shape. A workgroup owns 16 output columns (every row: M <= MR <= 8) and NW
 // waves. Groups are independent until their folds, so the waves split K
 // instead of the columns: in a round of RK elements of K, wave w computes P
 // and X of the groups in its BPW consecutive 128-element blocks and leaves
-// them in LDS; after a barrier wave 0 folds the round's groups in ascending
-// order, one output element per lane (lane 16 e + n: row e, column n), and
-// carries acc into the next round.
+// them in LDS; after a barrier waves 0 .. GR - 1 fold the round's groups in
+// ascending order, one output element per lane (wave w, lane 16 e + n: row
+// 4 w + e, column n), and carry acc into the next round.
 //
 // Feed. All of a round's loads are issued at its start, in the order x,
 // codes, scales and biases, so each wait lets the later loads stay in
@@ -44,14 +44,16 @@ struct QDecode {
   static constexpr int SPL = 16 * RG / NT;    // scale (and bias) entries per thread
   static_assert((RK / 8) % NT == 0 && (16 * RG) % NT == 0 && BPW >= 1, "round split");
   static_assert(GS >= 32 && GS <= 128, "groups of one to four chunk-steps: a block holds whole groups");
-  static_assert(MR >= 1 && MR <= 4, "one to four rows");
+  static_assert(MR >= 1 && MR <= 8, "one to eight rows");
   // LDS: x rows; P of each group (rows 0 .. MR - 1, 16 columns, [row][column]);
-  // X of each group (rows 0 .. MR - 1); scales and biases as fp32, a row per
+  // X of each group (rows 0 .. 4 GR - 1); scales and biases as fp32, a row per
   // column; and 256 bytes that lanes with nothing to store write to instead
   // (so the stores need no branch; nothing reads them).
+  static constexpr int GR = (MR + 3) / 4;     // lane groups whose MFMA rows are rows of x
+  static constexpr int XS = 16 * GR;          // bytes of X per group
   static constexpr int OFF_P = MR * XROW;
   static constexpr int OFF_X = OFF_P + RG * MR * 64;
-  static constexpr int OFF_S = OFF_X + RG * 16;
+  static constexpr int OFF_S = OFF_X + RG * XS;
   static constexpr int OFF_Z = OFF_S + 16 * SRS * 4;
   static constexpr int OFF_DUMMY = OFF_Z + 16 * SRS * 4;
   static constexpr int LDS_BYTES = OFF_DUMMY + 256;
@@ -88,7 +90,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
   const uint4 ones = make_uint4(ONE, ONE, ONE, ONE);
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
 
-  float acc = 0.f;  // wave 0: element (row lane / 16, column lane % 16)
+  float acc = 0.f;  // waves w < GR: element (row 4 w + lane / 16, column lane % 16)
   const int64_t rounds = (K + RK - 1) / RK;
   for (int64_t rr = 0; rr < rounds; rr++) {
     // The round index passes through an empty asm statement: nothing below
@@ -141,16 +143,17 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
     // This wave's groups: P and X of each into LDS. The x operands of a
     // block are read while the previous block computes; when all of the
     // wave's blocks lie inside K (FULL) the blocks run without bound tests.
-    // Lane group 0 stores P (rows 0 .. MR - 1 of its column), lane 0 stores
-    // X; every other lane stores into its own 4 bytes of the dummy area. (The
-    // masks pass through an empty asm statement so that each store address is
-    // computed where it is used.)
+    // Lane groups g < GR store P (rows 4 g .. 4 g + 3 of their column, those
+    // below MR), their lane 0 stores X; every other lane stores into its own 4
+    // bytes of the dummy area. (The masks pass through an empty asm statement
+    // so that each store address is computed where it is used.)
     const int64_t q0 = k0 >> 5;              // the round's first chunk-step
     const int64_t qw = q0 + 4 * wave * BPW;  // this wave's first chunk-step
-    uint32_t p_at = g == 0 ? (uint32_t)(D::OFF_P + r16 * 4) : (uint32_t)(D::OFF_DUMMY + lane * 4);
-    uint32_t p_gmask = g == 0 ? ~0u : 0u;
-    uint32_t x_at = lane == 0 ? (uint32_t)D::OFF_X : (uint32_t)(D::OFF_DUMMY + lane * 4);
-    uint32_t x_gmask = lane == 0 ? ~0u : 0u;
+    const bool prow = g < D::GR, xrow = prow && r16 == 0;
+    uint32_t p_at = prow ? (uint32_t)(D::OFF_P + g * 256 + r16 * 4) : (uint32_t)(D::OFF_DUMMY + lane * 4);
+    uint32_t p_gmask = prow ? ~0u : 0u;
+    uint32_t x_at = xrow ? (uint32_t)(D::OFF_X + g * 16) : (uint32_t)(D::OFF_DUMMY + lane * 4);
+    uint32_t x_gmask = xrow ? ~0u : 0u;
     asm volatile("" : "+v"(p_gmask), "+v"(x_gmask), "+v"(p_at), "+v"(x_at));
     const auto blocks = [&](auto full_tag) {
       constexpr bool FULL = decltype(full_tag)::value;
@@ -179,9 +182,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
           if ((jj % CPG) == CPG - 1) {
             const uint32_t gi = (uint32_t)((q - q0) / CPG);
 #pragma unroll
-            for (int e = 0; e < MR; e++) {
+            for (int e = 0; e < (MR < 4 ? MR : 4); e++) {
               *reinterpret_cast<float*>(lds + p_at + ((gi * (MR * 64) + e * 64) & p_gmask)) = P[e];
-              *reinterpret_cast<float*>(lds + x_at + ((gi * 16 + e * 4) & x_gmask)) = X[e];
+              *reinterpret_cast<float*>(lds + x_at + ((gi * D::XS + e * 4) & x_gmask)) = X[e];
             }
           }
         }
@@ -203,16 +206,16 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    if (wave == 0) {
+    if (wave < D::GR) {
       // The round's groups in ascending order, FC at a time, the operands of
-      // the next FC read while these fold.
+      // the next FC read while these fold; wave w folds rows 4 w .. 4 w + 3.
       constexpr int FC = 8;
-      const int e = lane >> 4, n = lane & 15;
+      const int e = 4 * wave + (lane >> 4), n = lane & 15;
       const int ng = (int)min((int64_t)RG, G - r * RG);
       uint32_t op = D::OFF_P + (e * 16 + n) * 4, ox = D::OFF_X + e * 4, os = n * D::SRS * 4;
       asm volatile("" : "+v"(op), "+v"(ox), "+v"(os));
       const float* Pf = reinterpret_cast<const float*>(lds + op);  // group gi: [MR * 16 gi]
-      const float* Xf = reinterpret_cast<const float*>(lds + ox);  // [4 gi]
+      const float* Xf = reinterpret_cast<const float*>(lds + ox);  // [XS / 4 gi]
       const f32x4_t* Sf = reinterpret_cast<const f32x4_t*>(lds + D::OFF_S + os);
       const f32x4_t* Zf = reinterpret_cast<const f32x4_t*>(lds + D::OFF_Z + os);
       struct Ops {
@@ -223,7 +226,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < FC; i++) {
           o.p[i] = Pf[(c * FC + i) * MR * 16];
-          o.x[i] = Xf[(c * FC + i) * 4];
+          o.x[i] = Xf[(c * FC + i) * (D::XS / 4)];
         }
 #pragma unroll
         for (int i = 0; i < FC / 4; i++) {
@@ -253,14 +256,14 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
       const float* Zs = reinterpret_cast<const float*>(Zf);
       for (int gi = nfull * FC; gi < ng; gi++) {
         acc = __builtin_fmaf(Ss[gi], Pf[gi * MR * 16], acc);
-        acc = __builtin_fmaf(Zs[gi], Xf[gi * 4], acc);
+        acc = __builtin_fmaf(Zs[gi], Xf[gi * (D::XS / 4)], acc);
       }
     }
     if (rr + 1 < rounds) asm volatile("s_barrier" ::: "memory");
   }
 
-  if (wave == 0) {
-    const int e = lane >> 4, n = lane & 15;
+  if (wave < D::GR) {
+    const int e = 4 * wave + (lane >> 4), n = lane & 15;
     if (e < mrows && n < cols) static_cast<T*>(p.out)[e * N + n0 + n] = Elem<T>::from_f32(acc);
   }
 }
