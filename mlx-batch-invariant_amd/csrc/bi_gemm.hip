@@ -135,16 +135,21 @@ int pick_geometry(int64_t M, int64_t N, int dtype, int trans_b) {
 // dense rules, except that 128 x 128 must fill the CUs (its workgroups
 // dequantize twice the columns: N = 11008, M = 256: 64 x 64 61 us, 128 x 128
 // 70 us).
-// Id of the quantized decode footprint (bi_gemm_qdecode.h: 4-bit codes, at
-// most 8 rows), one past the dense table.
+// Id of the quantized decode footprint (bi_gemm_qdecode.h: 4- or 8-bit
+// codes, at most 8 rows), one past the dense table.
 constexpr int kQDecode = kNumGeometries;
 
-int pick_qgeometry(int64_t M, int64_t N, int bits) {
-  // The decode footprint: up to 4 rows everywhere; 5-8 rows (an LDS share
-  // and register count that fit one workgroup per CU) only while the column
-  // blocks fit one round over the 256 CUs (N = 4096, M = 8: 7.3 against 9.3
-  // us; N = 11008: 18.5 against 13.6 us).
-  if (bits == 4 && (M <= 4 || (M <= 8 && ceil_div(N, 16) <= 256))) return kQDecode;
+int pick_qgeometry(int64_t M, int64_t N, int64_t K, int bits) {
+  // The decode footprint. 4-bit: up to 4 rows everywhere; 5-8 rows (an LDS
+  // share and register count that fit one workgroup per CU) only while the
+  // column blocks fit one round over the 256 CUs (N = 4096, M = 8: 7.3
+  // against 9.3 us; N = 11008: 18.5 against 13.6 us). 8-bit: one row
+  // everywhere (N = 32000: 29.5 against 33.1 us); up to 8 rows only with one
+  // round of column blocks and of K (N = K = 4096, M = 8: 8.5 against 9.4 us;
+  // K = 11008, M = 4: 21.3 against 19.8 us).
+  const bool one_round = ceil_div(N, 16) <= 256;
+  if (bits == 4 && (M <= 4 || (M <= 8 && one_round))) return kQDecode;
+  if (bits == 8 && (M == 1 || (M <= 8 && one_round && K <= 4096))) return kQDecode;
   if (M <= 16) return 0;
   const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);
   const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
@@ -405,11 +410,11 @@ int qvalidate(const void* x, const void* w, const void* scales, const void* bias
 int qlaunch_decode(const void* x, const void* w, const void* scales, const void* biases,
                    void* out, int64_t M, int64_t N, int64_t K, int group_size, int bits,
                    int dtype, void* stream) {
-  if (bits != 4 || M > 8)
+  if ((bits != 4 && bits != 8) || M > 8)
     return bi::fail(BI_EUNSUPPORTED,
-                    "bi_qgemm: the decode footprint takes 4-bit weights and at most 8 rows");
+                    "bi_qgemm: the decode footprint takes 4- and 8-bit weights and at most 8 rows");
   const int64_t lim = (int64_t)1 << 31;
-  if (M * K * 2 >= lim || 16 * K / 2 >= lim)
+  if (M * K * 2 >= lim || 16 * K * bits / 8 >= lim)
     return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: operand panel of 2 GiB or more");
   GemmArgs p = {};
   p.a = x;
@@ -423,8 +428,8 @@ int qlaunch_decode(const void* x, const void* w, const void* scales, const void*
   p.qgroup_shift = group_shift(group_size);
   const int64_t blocks = ceil_div(N, 16);
   if (blocks > INT32_MAX) return bi::fail(BI_EINVAL, "bi_qgemm: too many tiles");
-  KernelFn fn = dtype == BI_F16 ? bi_qdecode_kernel_f16(group_size, (int)M)
-                                : bi_qdecode_kernel_bf16(group_size, (int)M);
+  KernelFn fn = dtype == BI_F16 ? bi_qdecode_kernel_f16(group_size, (int)M, bits)
+                                : bi_qdecode_kernel_bf16(group_size, (int)M, bits);
   if (!fn) return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: decode footprint not built");
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(64 * bi_gemm_dev::kQDecodeWaves),
                      0, static_cast<hipStream_t>(stream), p);
@@ -478,7 +483,7 @@ extern "C" int bi_qgemm(const void* x, const void* w, const void* scales, const 
   const int rc = qvalidate(x, w, scales, biases, out, M, N, K, group_size, bits, dtype);
   if (rc != BI_OK || M == 0 || N == 0) return rc;
   return qlaunch(x, w, scales, biases, out, M, N, K, group_size, bits, dtype,
-                 pick_qgeometry(M, N, bits), hip_stream);
+                 pick_qgeometry(M, N, K, bits), hip_stream);
 }
 
 extern "C" int bi_qgemm_num_geometries(void) { return kQDecode + 1; }

@@ -149,6 +149,27 @@ __device__ __forceinline__ uint4 codes_as_elems(uint32_t w) {
   return r;
 }
 
+// The 8 8-bit codes of words lo (codes 0-3, code t in byte t) and hi (codes
+// 4-7) as element-type integers (0 .. 255 are exact in bf16 and f16), two per
+// register, code 0 in the low half of the first: one v_cvt_f32_ubyte<b> per
+// code and one pack per pair.
+template <typename T>
+__device__ __forceinline__ uint4 bytes_as_elems(uint32_t lo, uint32_t hi) {
+  const auto pack = [](float c0, float c1) -> uint32_t {
+    if constexpr (IsBF16<T>::value)  // the top halves of the fp32 values (exact: <= 8 bits)
+      return __builtin_amdgcn_perm(__float_as_uint(c1), __float_as_uint(c0), 0x07060302u);
+    else
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(c0, c1));
+  };
+  const auto byte = [](uint32_t d, int b) -> float { return (float)((d >> (8 * b)) & 0xFFu); };
+  uint4 r;
+  r.x = pack(byte(lo, 0), byte(lo, 1));
+  r.y = pack(byte(lo, 2), byte(lo, 3));
+  r.z = pack(byte(hi, 0), byte(hi, 1));
+  r.w = pack(byte(hi, 2), byte(hi, 3));
+  return r;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
 // Remap so that consecutive logical tiles -- which share operand panels -- run
 // on the same XCD.
@@ -1542,23 +1563,31 @@ KernelFn qkernel_for(int g, int bits, int group) {
   return nullptr;
 }
 
-// The quantized decode footprint (4-bit codes, at most 8 rows) for group size
-// `group` and `rows` rows of x, kQDecodeWaves waves per workgroup.
+// The quantized decode footprint (4- or 8-bit codes, at most 8 rows) for
+// group size `group` and `rows` rows of x, kQDecodeWaves waves per workgroup.
 constexpr int kQDecodeWaves = 4;
-template <typename T, int GS>
+template <typename T, int GS, int QB>
 KernelFn qdecode_kernel_rows(int rows) {
   constexpr int NW = kQDecodeWaves;
-  if (rows <= 1) return gemm_qdecode_kernel<T, GS, 1, NW>;
-  if (rows == 2) return gemm_qdecode_kernel<T, GS, 2, NW>;
-  if (rows <= 4) return gemm_qdecode_kernel<T, GS, 4, NW>;
-  return gemm_qdecode_kernel<T, GS, 8, NW>;
+  if (rows <= 1) return gemm_qdecode_kernel<T, GS, 1, NW, QB>;
+  if (rows == 2) return gemm_qdecode_kernel<T, GS, 2, NW, QB>;
+  if (rows <= 4) return gemm_qdecode_kernel<T, GS, 4, NW, QB>;
+  return gemm_qdecode_kernel<T, GS, 8, NW, QB>;
+}
+template <typename T, int QB>
+KernelFn qdecode_kernel_group(int group, int rows) {
+  switch (group) {
+    case 32: return qdecode_kernel_rows<T, 32, QB>(rows);
+    case 64: return qdecode_kernel_rows<T, 64, QB>(rows);
+    case 128: return qdecode_kernel_rows<T, 128, QB>(rows);
+  }
+  return nullptr;
 }
 template <typename T>
-KernelFn qdecode_kernel_for(int group, int rows) {
-  switch (group) {
-    case 32: return qdecode_kernel_rows<T, 32>(rows);
-    case 64: return qdecode_kernel_rows<T, 64>(rows);
-    case 128: return qdecode_kernel_rows<T, 128>(rows);
+KernelFn qdecode_kernel_for(int group, int rows, int bits) {
+  switch (bits) {
+    case 4: return qdecode_kernel_group<T, 4>(group, rows);
+    case 8: return qdecode_kernel_group<T, 8>(group, rows);
   }
   return nullptr;
 }
@@ -1571,5 +1600,5 @@ bi_gemm_dev::KernelFn bi_gemm_kernel_f16(int g, bool trans_b);
 bi_gemm_dev::KernelFn bi_gemm_kernel_bf16(int g, bool trans_b);
 bi_gemm_dev::KernelFn bi_qgemm_kernel_f16(int g, int bits, int group);
 bi_gemm_dev::KernelFn bi_qgemm_kernel_bf16(int g, int bits, int group);
-bi_gemm_dev::KernelFn bi_qdecode_kernel_f16(int group, int rows);
-bi_gemm_dev::KernelFn bi_qdecode_kernel_bf16(int group, int rows);
+bi_gemm_dev::KernelFn bi_qdecode_kernel_f16(int group, int rows, int bits);
+bi_gemm_dev::KernelFn bi_qdecode_kernel_bf16(int group, int rows, int bits);

@@ -1,5 +1,5 @@
-// The quantized decode footprint of the batch-invariant GEMM: 4-bit affine
-// weights, 16-bit activations, at most 8 rows of x. Included by
+// The quantized decode footprint of the batch-invariant GEMM: 4- and 8-bit
+// affine weights, 16-bit activations, at most 8 rows of x. Included by
 // bi_gemm_kernel.h; every element runs the quantized sequence of that file's
 // quantized section: per group of K, P = the group's chunk-steps (ascending,
 // the first from +0.0) of v_mfma_f32_16x16x32_{bf16,f16} on the x chunk and
@@ -20,13 +20,14 @@
 // flight: a wave works on its first block of codes while the others land.
 // x (rows 0 .. M - 1 of the round's K range) goes through registers into
 // LDS, rows padded by 64 bytes so the rows' operand reads fall on distinct
-// banks. Lane (g, n) of a wave reads the 16 bytes of block b's codes of
-// weight row n that hold chunk-step 4 b + g's four 32-bit words, one per
-// lane group; a 4 x 4 transpose across the lane groups (two rounds of
-// v_permlane32_swap / v_permlane16_swap) leaves in register j of lane group g
-// its word of chunk-step 4 b + j -- the 8 codes of k = 32 q + 8 g + t, t =
-// 0..7, the MFMA's B operand layout -- so every code load is a whole 16 bytes
-// and no code passes through LDS.
+// banks. Lane (g, n) of a wave reads the bytes of block b's codes of weight
+// row n that hold chunk-step 4 b + g (16 bytes at 4 bits: four 32-bit words,
+// one per lane group; 32 bytes at 8 bits: two words per lane group); a 4 x 4
+// transpose across the lane groups (two rounds of v_permlane32_swap /
+// v_permlane16_swap; at 8 bits one for the even and one for the odd words)
+// leaves in position j of lane group g its words of chunk-step 4 b + j -- the
+// 8 codes of k = 32 q + 8 g + t, t = 0..7, the MFMA's B operand layout -- so
+// every code load is whole 16-byte chunks and no code passes through LDS.
 #pragma once
 
 namespace bi_gemm_dev {
@@ -59,9 +60,12 @@ struct QDecode {
   static constexpr int LDS_BYTES = OFF_DUMMY + 256;
 };
 
-template <typename T, int GS, int MR, int NW>
+template <typename T, int GS, int MR, int NW, int QB>
 __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
+  static_assert(QB == 4 || QB == 8, "4- or 8-bit codes");
   using D = QDecode<GS, MR, NW>;
+  constexpr int WPL = QB / 4;       // words of a chunk-step per lane group: 4-bit 1, 8-bit 2
+  constexpr int CW = 4 * (QB / 4);  // code words a lane loads per block: 4 or 8
   constexpr int RK = D::RK, RG = D::RG, CPG = D::CPG, BPW = D::BPW, NT = D::NT;
   constexpr int64_t E = 2;
   __shared__ __attribute__((aligned(16))) char lds[D::LDS_BYTES];
@@ -74,7 +78,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
   const int64_t n0 = (int64_t)blockIdx.x * 16;
   const int64_t G = K / GS;         // groups
   const int64_t nq = K / 32;        // chunk-steps
-  const int64_t qrow = K / 2;       // bytes of packed codes per weight row
+  const int64_t qrow = K * QB / 8;  // bytes of packed codes per weight row
   const int64_t cols = min((int64_t)16, N - n0);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.a, M * K * E);
   const __amdgpu_buffer_rsrc_t rw =
@@ -111,16 +115,21 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
         const int64_t k = k0 + kc * 8;
         if (row < mrows) xv[row][i] = buffer_chunk(rx, k < K ? (uint32_t)((row * K + k) * E) : kOutOfRange);
       }
-    uint32_t cw[BPW][4];
+    // Lane (g, n) loads chunk-step 4 b + g's codes of weight row n: 16 bytes
+    // at 4 bits, 32 at 8 (a 32-element chunk-step is 4 QB words of the row).
+    uint32_t cw[BPW][CW];
 #pragma unroll
     for (int j = 0; j < BPW; j++) {
-      const int64_t q = (k0 >> 5) + 4 * (wave * BPW + j) + g;  // chunk-step this lane's 16 bytes hold
-      const uint32_t off = q < nq ? (uint32_t)(r16 * qrow + q * 16) : kOutOfRange;
-      const uint4 v = buffer_chunk(rw, off);
-      cw[j][0] = v.x;
-      cw[j][1] = v.y;
-      cw[j][2] = v.z;
-      cw[j][3] = v.w;
+      const int64_t q = (k0 >> 5) + 4 * (wave * BPW + j) + g;  // chunk-step this lane's bytes hold
+      const uint32_t off = q < nq ? (uint32_t)(r16 * qrow + q * (4 * QB)) : kOutOfRange;
+#pragma unroll
+      for (int h = 0; h < CW / 4; h++) {
+        const uint4 v = buffer_chunk(rw, off == kOutOfRange ? kOutOfRange : off + 16 * h);
+        cw[j][4 * h + 0] = v.x;
+        cw[j][4 * h + 1] = v.y;
+        cw[j][4 * h + 2] = v.z;
+        cw[j][4 * h + 3] = v.w;
+      }
     }
     unsigned short sv[D::SPL], zv[D::SPL];
 #pragma unroll
@@ -169,13 +178,26 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
         const int64_t qb = qw + 4 * j;
         if (!FULL && qb >= nq) break;
         if (j + 1 < BPW) read_x(j + 1, av[(j + 1) & 1]);
-        xpose_lane_groups(cw[j]);
+        // After the transposes word set u of lane group g holds, at position
+        // jj, its words of chunk-step 4 b + jj (4-bit: one word; 8-bit: the
+        // even set the first, the odd set the second).
+        uint32_t wu[WPL][4];
+#pragma unroll
+        for (int u = 0; u < WPL; u++) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) wu[u][i] = cw[j][WPL * i + u];
+          xpose_lane_groups(wu[u]);
+        }
         f32x4_t P = zero, X = zero;
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) {
           const int64_t q = qb + jj;
           if (!FULL && q >= nq) break;
-          const uint4 bv = codes_as_elems<T>(cw[j][jj]);
+          uint4 bv;
+          if constexpr (QB == 4)
+            bv = codes_as_elems<T>(wu[0][jj]);
+          else
+            bv = bytes_as_elems<T>(wu[0][jj], wu[1][jj]);
           const bool first = (jj % CPG) == 0;  // blocks start on group boundaries
           P = chunk_step(T(0), av[j & 1][jj], bv, first ? zero : P);
           X = chunk_step(T(0), av[j & 1][jj], ones, first ? zero : X);

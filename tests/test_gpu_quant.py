@@ -131,30 +131,32 @@ def test_every_geometry_gives_the_same_bits(cuda):
 
 @pytest.mark.parametrize("dname,dtype", QDTYPES)
 def test_decode_footprint_gives_the_same_bits(cuda, dname, dtype):
-    """The decode footprint (4-bit weights, at most 4 rows: the waves of a
-    workgroup split K by groups, the codes reach the matrix cores through a
+    """The decode footprint (4- and 8-bit weights, at most 8 rows: the waves of
+    a workgroup split K by groups, the codes reach the matrix cores through a
     transpose across lane groups) gives the 16x16 footprint's bits: one
     group, blocks cut short by K, K over several rounds, N not a multiple
-    of 16, one to eight rows. Other bit widths and more rows are refused."""
+    of 16, one to eight rows. 2-bit weights and more rows are refused."""
     L = _lib.lib()
     dec = L.bi_gemm_num_geometries()
     assert L.bi_qgemm_num_geometries() == dec + 1
-    for gs in (32, 64, 128):
-        for M, N, K in [(1, 37, gs), (2, 48, 3 * gs), (1, 272, 768), (4, 130, 4096),
-                        (3, 64, 8192 + 3 * gs), (1, 200, 4096 + gs), (5, 40, 256),
-                        (8, 96, 4096 + 5 * gs), (7, 33, 2 * gs)]:
-            q, s, b = _qweight(N, K, dtype, 120 + gs + M, gs, 4, cuda)
-            x = rn((M, K), dtype, 121 + K, device=cuda)
-            want = bits(_launch(L, x, q, s, b, gs, 4, 0))
-            got = bits(_launch(L, x, q, s, b, gs, 4, dec))
-            bad = int((got != want).sum())
-            assert bad == 0, "%s gs=%d M=%d N=%d K=%d: %d differ" % (dname, gs, M, N, K, bad)
+    for nbits in (4, 8):
+        for gs in (32, 64, 128):
+            for M, N, K in [(1, 37, gs), (2, 48, 3 * gs), (1, 272, 768), (4, 130, 4096),
+                            (3, 64, 8192 + 3 * gs), (1, 200, 4096 + gs), (5, 40, 256),
+                            (8, 96, 4096 + 5 * gs), (7, 33, 2 * gs)]:
+                q, s, b = _qweight(N, K, dtype, 120 + gs + M + nbits, gs, nbits, cuda)
+                x = rn((M, K), dtype, 121 + K, device=cuda)
+                want = bits(_launch(L, x, q, s, b, gs, nbits, 0))
+                got = bits(_launch(L, x, q, s, b, gs, nbits, dec))
+                bad = int((got != want).sum())
+                assert bad == 0, "%s bits=%d gs=%d M=%d N=%d K=%d: %d differ" % (
+                    dname, nbits, gs, M, N, K, bad)
     q, s, b = _qweight(64, 256, dtype, 122, 64, 4, cuda)
     with pytest.raises(NotImplementedError):
         _launch(L, rn((9, 256), dtype, 123, device=cuda), q, s, b, 64, 4, dec)
-    q, s, b = _qweight(64, 256, dtype, 124, 64, 8, cuda)
+    q, s, b = _qweight(64, 256, dtype, 124, 64, 2, cuda)
     with pytest.raises(NotImplementedError):
-        _launch(L, rn((1, 256), dtype, 125, device=cuda), q, s, b, 64, 8, dec)
+        _launch(L, rn((1, 256), dtype, 125, device=cuda), q, s, b, 64, 2, dec)
 
 
 @pytest.mark.parametrize("dname,dtype", QDTYPES)
