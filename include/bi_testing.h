@@ -65,7 +65,7 @@ int bi_feed_probe(const void* src, int64_t panel_bytes, int panels, int stages, 
 /* Number of geometries bi_qgemm_with_geometry accepts: the GEMM geometries
  * (bi_gemm_num_geometries()), then the quantized decode footprint, id
  * bi_gemm_num_geometries(): 16 output columns per workgroup whose waves split
- * K by groups (4- and 8-bit weights and at most 8 rows of x only; otherwise
+ * K by groups (at most 8 rows of x; otherwise
  * BI_EUNSUPPORTED). No counterpart in the reference. */
 int bi_qgemm_num_geometries(void);
 

@@ -148,7 +148,7 @@ int pick_qgeometry(int64_t M, int64_t N, int64_t K, int bits) {
   // round of column blocks and of K (N = K = 4096, M = 8: 8.5 against 9.4 us;
   // K = 11008, M = 4: 21.3 against 19.8 us).
   const bool one_round = ceil_div(N, 16) <= 256;
-  if (bits == 4 && (M <= 4 || (M <= 8 && one_round))) return kQDecode;
+  if ((bits == 4 || bits == 2) && (M <= 4 || (M <= 8 && one_round))) return kQDecode;
   if (bits == 8 && (M == 1 || (M <= 8 && one_round && K <= 4096))) return kQDecode;
   if (M <= 16) return 0;
   const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);
@@ -410,9 +410,7 @@ int qvalidate(const void* x, const void* w, const void* scales, const void* bias
 int qlaunch_decode(const void* x, const void* w, const void* scales, const void* biases,
                    void* out, int64_t M, int64_t N, int64_t K, int group_size, int bits,
                    int dtype, void* stream) {
-  if ((bits != 4 && bits != 8) || M > 8)
-    return bi::fail(BI_EUNSUPPORTED,
-                    "bi_qgemm: the decode footprint takes 4- and 8-bit weights and at most 8 rows");
+  if (M > 8) return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: the decode footprint takes at most 8 rows");
   const int64_t lim = (int64_t)1 << 31;
   if (M * K * 2 >= lim || 16 * K * bits / 8 >= lim)
     return bi::fail(BI_EUNSUPPORTED, "bi_qgemm: operand panel of 2 GiB or more");

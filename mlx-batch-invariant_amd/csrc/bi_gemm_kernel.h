@@ -149,6 +149,36 @@ __device__ __forceinline__ uint4 codes_as_elems(uint32_t w) {
   return r;
 }
 
+// The 8 2-bit codes in the low 16 bits of v (code t in bits 2t, 2t + 1) as
+// element-type integers, two per register, code 0 in the low half of the
+// first. Each byte of codes spreads into four bytes by OR-ing shifted copies
+// (u | u << 6 | u << 12 | u << 18 puts code i of u in bits 8i, 8i + 1 and
+// no other code there; OR, not a sum, so nothing carries), masked to two bits;
+// 0-3 read as fp8 E4M3 are q * 2^-9, so the scaled conversion with scale 2^9
+// yields them exactly, two codes per instruction.
+template <typename T>
+__device__ __forceinline__ uint4 codes2_as_elems(uint32_t v) {
+  const auto spread = [](uint32_t u) -> uint32_t {
+    u = u | (u << 6);
+    u = u | (u << 12);
+    return u & 0x03030303u;
+  };
+  const uint32_t lo = spread(v & 0xFFu), hi = spread((v >> 8) & 0xFFu);
+  uint4 r;
+  if constexpr (IsBF16<T>::value) {
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, true));
+  } else {
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true));
+  }
+  return r;
+}
+
 // The 8 8-bit codes of words lo (codes 0-3, code t in byte t) and hi (codes
 // 4-7) as element-type integers (0 .. 255 are exact in bf16 and f16), two per
 // register, code 0 in the low half of the first: one v_cvt_f32_ubyte<b> per
@@ -1563,7 +1593,7 @@ KernelFn qkernel_for(int g, int bits, int group) {
   return nullptr;
 }
 
-// The quantized decode footprint (4- or 8-bit codes, at most 8 rows) for
+// The quantized decode footprint (2-, 4- or 8-bit codes, at most 8 rows) for
 // group size `group` and `rows` rows of x, kQDecodeWaves waves per workgroup.
 constexpr int kQDecodeWaves = 4;
 template <typename T, int GS, int QB>
@@ -1586,6 +1616,7 @@ KernelFn qdecode_kernel_group(int group, int rows) {
 template <typename T>
 KernelFn qdecode_kernel_for(int group, int rows, int bits) {
   switch (bits) {
+    case 2: return qdecode_kernel_group<T, 2>(group, rows);
     case 4: return qdecode_kernel_group<T, 4>(group, rows);
     case 8: return qdecode_kernel_group<T, 8>(group, rows);
   }

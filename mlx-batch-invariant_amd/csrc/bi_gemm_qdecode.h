@@ -1,5 +1,5 @@
-// The quantized decode footprint of the batch-invariant GEMM: 4- and 8-bit
-// affine weights, 16-bit activations, at most 8 rows of x. Included by
+// The quantized decode footprint of the batch-invariant GEMM: 2-, 4- and
+// 8-bit affine weights, 16-bit activations, at most 8 rows of x. Included by
 // bi_gemm_kernel.h; every element runs the quantized sequence of that file's
 // quantized section: per group of K, P = the group's chunk-steps (ascending,
 // the first from +0.0) of v_mfma_f32_16x16x32_{bf16,f16} on the x chunk and
@@ -22,12 +22,14 @@
 // LDS, rows padded by 64 bytes so the rows' operand reads fall on distinct
 // banks. Lane (g, n) of a wave reads the bytes of block b's codes of weight
 // row n that hold chunk-step 4 b + g (16 bytes at 4 bits: four 32-bit words,
-// one per lane group; 32 bytes at 8 bits: two words per lane group); a 4 x 4
-// transpose across the lane groups (two rounds of v_permlane32_swap /
+// one per lane group; 32 bytes at 8 bits: two words per lane group; 8 bytes at
+// 2 bits: 16 bits per lane group, widened to a word each); a 4 x 4 transpose
+// across the lane groups (two rounds of v_permlane32_swap /
 // v_permlane16_swap; at 8 bits one for the even and one for the odd words)
 // leaves in position j of lane group g its words of chunk-step 4 b + j -- the
 // 8 codes of k = 32 q + 8 g + t, t = 0..7, the MFMA's B operand layout -- so
-// every code load is whole 16-byte chunks and no code passes through LDS.
+// every code load is whole 16-byte chunks (8 bytes at 2 bits) and no code
+// passes through LDS.
 #pragma once
 
 namespace bi_gemm_dev {
@@ -62,10 +64,12 @@ struct QDecode {
 
 template <typename T, int GS, int MR, int NW, int QB>
 __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
-  static_assert(QB == 4 || QB == 8, "4- or 8-bit codes");
+  static_assert(QB == 2 || QB == 4 || QB == 8, "2-, 4- or 8-bit codes");
   using D = QDecode<GS, MR, NW>;
-  constexpr int WPL = QB / 4;       // words of a chunk-step per lane group: 4-bit 1, 8-bit 2
-  constexpr int CW = 4 * (QB / 4);  // code words a lane loads per block: 4 or 8
+  // Words of a chunk-step per lane group: 2-bit half a word (widened to one
+  // below), 4-bit 1, 8-bit 2; code words a lane loads per block: 2, 4 or 8.
+  constexpr int WPL = QB == 8 ? 2 : 1;
+  constexpr int CW = QB == 8 ? 8 : QB == 4 ? 4 : 2;
   constexpr int RK = D::RK, RG = D::RG, CPG = D::CPG, BPW = D::BPW, NT = D::NT;
   constexpr int64_t E = 2;
   __shared__ __attribute__((aligned(16))) char lds[D::LDS_BYTES];
@@ -122,13 +126,19 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
     for (int j = 0; j < BPW; j++) {
       const int64_t q = (k0 >> 5) + 4 * (wave * BPW + j) + g;  // chunk-step this lane's bytes hold
       const uint32_t off = q < nq ? (uint32_t)(r16 * qrow + q * (4 * QB)) : kOutOfRange;
+      if constexpr (QB == 2) {
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, (int)off, 0, 0));
+        cw[j][0] = v.x;
+        cw[j][1] = v.y;
+      } else {
 #pragma unroll
-      for (int h = 0; h < CW / 4; h++) {
-        const uint4 v = buffer_chunk(rw, off == kOutOfRange ? kOutOfRange : off + 16 * h);
-        cw[j][4 * h + 0] = v.x;
-        cw[j][4 * h + 1] = v.y;
-        cw[j][4 * h + 2] = v.z;
-        cw[j][4 * h + 3] = v.w;
+        for (int h = 0; h < CW / 4; h++) {
+          const uint4 v = buffer_chunk(rw, off == kOutOfRange ? kOutOfRange : off + 16 * h);
+          cw[j][4 * h + 0] = v.x;
+          cw[j][4 * h + 1] = v.y;
+          cw[j][4 * h + 2] = v.z;
+          cw[j][4 * h + 3] = v.w;
+        }
       }
     }
     unsigned short sv[D::SPL], zv[D::SPL];
@@ -182,11 +192,19 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
         // jj, its words of chunk-step 4 b + jj (4-bit: one word; 8-bit: the
         // even set the first, the odd set the second).
         uint32_t wu[WPL][4];
+        if constexpr (QB == 2) {
+          // Lane group i's 16 bits of chunk-step 4 b + g are half i % 2 of
+          // word i / 2: widened to a word each before the transpose.
 #pragma unroll
-        for (int u = 0; u < WPL; u++) {
+          for (int i = 0; i < 4; i++) wu[0][i] = (cw[j][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+          xpose_lane_groups(wu[0]);
+        } else {
 #pragma unroll
-          for (int i = 0; i < 4; i++) wu[u][i] = cw[j][WPL * i + u];
-          xpose_lane_groups(wu[u]);
+          for (int u = 0; u < WPL; u++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) wu[u][i] = cw[j][WPL * i + u];
+            xpose_lane_groups(wu[u]);
+          }
         }
         f32x4_t P = zero, X = zero;
 #pragma unroll
@@ -194,7 +212,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_qdecode_kernel(GemmArgs p) {
           const int64_t q = qb + jj;
           if (!FULL && q >= nq) break;
           uint4 bv;
-          if constexpr (QB == 4)
+          if constexpr (QB == 2)
+            bv = codes2_as_elems<T>(wu[0][jj]);
+          else if constexpr (QB == 4)
             bv = codes_as_elems<T>(wu[0][jj]);
           else
             bv = bytes_as_elems<T>(wu[0][jj], wu[1][jj]);

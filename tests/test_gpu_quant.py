@@ -131,15 +131,15 @@ def test_every_geometry_gives_the_same_bits(cuda):
 
 @pytest.mark.parametrize("dname,dtype", QDTYPES)
 def test_decode_footprint_gives_the_same_bits(cuda, dname, dtype):
-    """The decode footprint (4- and 8-bit weights, at most 8 rows: the waves of
+    """The decode footprint (2-, 4- and 8-bit weights, at most 8 rows: the waves of
     a workgroup split K by groups, the codes reach the matrix cores through a
     transpose across lane groups) gives the 16x16 footprint's bits: one
     group, blocks cut short by K, K over several rounds, N not a multiple
-    of 16, one to eight rows. 2-bit weights and more rows are refused."""
+    of 16, one to eight rows. More rows are refused."""
     L = _lib.lib()
     dec = L.bi_gemm_num_geometries()
     assert L.bi_qgemm_num_geometries() == dec + 1
-    for nbits in (4, 8):
+    for nbits in (2, 4, 8):
         for gs in (32, 64, 128):
             for M, N, K in [(1, 37, gs), (2, 48, 3 * gs), (1, 272, 768), (4, 130, 4096),
                             (3, 64, 8192 + 3 * gs), (1, 200, 4096 + gs), (5, 40, 256),
@@ -154,9 +154,6 @@ def test_decode_footprint_gives_the_same_bits(cuda, dname, dtype):
     q, s, b = _qweight(64, 256, dtype, 122, 64, 4, cuda)
     with pytest.raises(NotImplementedError):
         _launch(L, rn((9, 256), dtype, 123, device=cuda), q, s, b, 64, 4, dec)
-    q, s, b = _qweight(64, 256, dtype, 124, 64, 2, cuda)
-    with pytest.raises(NotImplementedError):
-        _launch(L, rn((1, 256), dtype, 125, device=cuda), q, s, b, 64, 2, dec)
 
 
 @pytest.mark.parametrize("dname,dtype", QDTYPES)
