@@ -135,15 +135,17 @@ int pick_geometry(int64_t M, int64_t N, int dtype, int trans_b) {
 // dense rules, except that 128 x 128 must fill the CUs (its workgroups
 // dequantize twice the columns: N = 11008, M = 256: 64 x 64 61 us, 128 x 128
 // 70 us).
-// Id of the quantized decode footprint (bi_gemm_qdecode.h: 4- or 8-bit
+// Id of the quantized decode footprint (bi_gemm_qdecode.h: 2-, 4- or 8-bit
 // codes, at most 8 rows), one past the dense table.
 constexpr int kQDecode = kNumGeometries;
 
 int pick_qgeometry(int64_t M, int64_t N, int64_t K, int bits) {
-  // The decode footprint. 4-bit: up to 4 rows everywhere; 5-8 rows (an LDS
-  // share and register count that fit one workgroup per CU) only while the
-  // column blocks fit one round over the 256 CUs (N = 4096, M = 8: 7.3
-  // against 9.3 us; N = 11008: 18.5 against 13.6 us). 8-bit: one row
+  // The decode footprint. 2- and 4-bit: up to 4 rows everywhere; 5-8 rows
+  // (an LDS share and register count that fit one workgroup per CU) only
+  // while the column blocks fit one round over the 256 CUs (4-bit, N = 4096,
+  // M = 8: 7.3 against 9.3 us; N = 11008: 18.5 against 13.6 us; 2-bit,
+  // N = 4096, M = 8: 7.5 against 10.3 us; N = 11008: 19.0 against 14.1 us).
+  // 8-bit: one row
   // everywhere (N = 32000: 29.5 against 33.1 us); up to 8 rows only with one
   // round of column blocks and of K (N = K = 4096, M = 8: 8.5 against 9.4 us;
   // K = 11008, M = 4: 21.3 against 19.8 us).
