@@ -69,6 +69,11 @@ int bi_feed_probe(const void* src, int64_t panel_bytes, int panels, int stages, 
  * BI_EUNSUPPORTED). No counterpart in the reference. */
 int bi_qgemm_num_geometries(void);
 
+/* The geometry bi_qgemm would launch for this problem (an id as for
+ * bi_qgemm_with_geometry); BI_EINVAL for bits other than 2, 4 and 8. No
+ * counterpart in the reference. */
+int bi_qgemm_pick_geometry(int64_t M, int64_t N, int64_t K, int bits);
+
 /* bi_qgemm with the geometry forced to `g` (same arguments and semantics). */
 int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
                            const void* biases, void* out, int64_t M, int64_t N, int64_t K,

@@ -488,6 +488,12 @@ extern "C" int bi_qgemm(const void* x, const void* w, const void* scales, const 
 
 extern "C" int bi_qgemm_num_geometries(void) { return kQDecode + 1; }
 
+extern "C" int bi_qgemm_pick_geometry(int64_t M, int64_t N, int64_t K, int bits) {
+  if (bits != 2 && bits != 4 && bits != 8)
+    return bi::fail(BI_EINVAL, "bi_qgemm: bits must be 2, 4 or 8, got %d", bits);
+  return pick_qgeometry(M, N, K, bits);
+}
+
 extern "C" int bi_qgemm_with_geometry(const void* x, const void* w, const void* scales,
                                       const void* biases, void* out, int64_t M, int64_t N,
                                       int64_t K, int group_size, int bits, int dtype, int g,

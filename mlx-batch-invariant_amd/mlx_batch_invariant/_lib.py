@@ -48,6 +48,7 @@ SIGNATURES = {
     "bi_qgemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                           _c_int, _c_int, _c_vp]),
     "bi_qgemm_num_geometries": (_c_int, []),
+    "bi_qgemm_pick_geometry": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "bi_qgemm_with_geometry": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                         _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "bi_sdpa_pick_shape": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,

@@ -94,6 +94,37 @@ def test_footprint_policy():
     assert pick(128, 4096, _lib.F32) == (64, 32, 8)
 
 
+def test_quantized_footprint_policy():
+    """The footprint bi_qgemm picks (a performance policy measured on MI355X;
+    every footprint gives the same bits, which the GPU tests prove): the
+    decode footprint for few rows, by code width and by whether its column
+    blocks fit one round over the CUs, the dense table's footprints above."""
+    L = _lib.lib()
+    geos = bi.geometries()
+    decode = L.bi_qgemm_num_geometries() - 1
+    assert decode == len(geos)
+
+    def pick(M, N, K=4096, bits=4):
+        g = L.bi_qgemm_pick_geometry(M, N, K, bits)
+        assert 0 <= g <= decode
+        return "decode" if g == decode else geos[g]
+
+    for bits in (2, 4):
+        for M in (1, 4):
+            assert pick(M, 4096, bits=bits) == pick(M, 32000, 11008, bits) == "decode"
+        assert pick(8, 4096, bits=bits) == "decode"              # 256 column blocks: one round
+        assert pick(5, 4112, bits=bits) == (16, 16, 4)           # 257 column blocks
+        assert pick(9, 4096, bits=bits) == (16, 16, 4)           # at most 8 rows
+    assert pick(1, 32000, 11008, bits=8) == "decode"
+    assert pick(8, 4096, bits=8) == "decode"
+    assert pick(2, 4096, 11008, bits=8) == (16, 16, 4)           # two rounds of K
+    assert pick(2, 11008, bits=8) == (16, 16, 4)
+    assert pick(32, 4096) == (16, 16, 4)
+    assert pick(32, 32000) == pick(256, 11008) == (64, 64, 8)
+    assert pick(256, 32000) == (128, 128, 8)
+    assert L.bi_qgemm_pick_geometry(1, 4096, 4096, 3) == _lib.EINVAL
+
+
 def _err():
     return _lib.lib().bi_last_error().decode()
 
